@@ -1,0 +1,169 @@
+/*
+ * qa.h -- C ABI of the MI355X (gfx950) linear-layer GEMM path of
+ * eclipse005/qwen3-aligner-wgpu.
+ *
+ * The reference dispatches every dense projection of its prefill forward
+ * through one WGSL GEMM family, `prefill_gemm` (src/shaders.rs:1785-2077), from
+ * two call surfaces: the text decoder's `gemm!` / `gemm_at!` macros
+ * (src/decoder.rs:1030-1104, uniform `GDims` at src/decoder.rs:194-212) and the
+ * audio tower's `GpuAudioEncoder::{gemm, gemm_beta, gemm_conv, dispatch_gemm}`
+ * (src/audio_encoder_gpu.rs:1614-1944).  Buffers come from `Gpu::storage`
+ * (src/gpu.rs:672-682), data moves with `Gpu::upload` / `write_at` /
+ * `readback` (src/gpu.rs:697-762) and `flush` / `pump` wait for the queue
+ * (src/gpu.rs:709-728).  This header is the C replacement for exactly that
+ * surface, so a Rust `extern "C"` shim can swap the bodies of those helpers.
+ *
+ * Conventions:
+ *  - Every function returns an int status: QA_OK (0) or a negative QA_E*
+ *    code; the message of the last failure on the calling thread is
+ *    qa_last_error().  Shapes are validated synchronously, before any launch;
+ *    launches are asynchronous on the context's one in-order stream, so an
+ *    asynchronous device fault surfaces at qa_sync (as it does at the
+ *    reference's poll, src/decoder.rs:1670-1672).
+ *  - All strides and sizes are in ELEMENTS (16-bit values).  The reference's
+ *    GDims carries bsa/bsb in u32 words but bsc in elements
+ *    (src/shaders.rs:1805-1810); a caller converting from GDims doubles
+ *    bsa/bsb.
+ *  - 16-bit data is little-endian f16 or bf16 bits, the reference's storage
+ *    format (src/shaders.rs:27-97, src/half16.rs:22-84).  The format is a
+ *    per-call field, not the process-wide setting of src/shaders.rs:99-158.
+ *  - A context owns one in-order HIP stream and is not safe for concurrent
+ *    calls; separate contexts on separate threads are (the reference records
+ *    its dispatches on one thread into one queue, src/align_inference.rs:485).
+ */
+#ifndef QA_H
+#define QA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QA_ABI_VERSION 1
+
+typedef struct qa_ctx qa_ctx;
+
+/* Status codes (the reference's anyhow errors, src/decoder.rs:927-950). */
+enum {
+  QA_OK = 0,
+  QA_EINVAL = -1,       /* bad argument or shape                          */
+  QA_ENOMEM = -2,       /* device allocation failed                       */
+  QA_EDEVICE = -3,      /* no usable device, or a HIP runtime failure      */
+  QA_EUNSUPPORTED = -4  /* valid request this build does not implement     */
+};
+
+/* 16-bit storage formats (src/shaders.rs:27-40, `Half`). */
+enum { QA_F16 = 0, QA_BF16 = 1 };
+
+/* qa_linear_desc.flags */
+enum {
+  /* C = round(acc + bias + C_old): the `beta = 1` residual form
+   * (src/shaders.rs:2067-2072; `gemm_acc`, src/decoder.rs:1602-1608,1652-1657;
+   * `gemm_beta`, src/audio_encoder_gpu.rs:1614-1632). */
+  QA_ACCUMULATE = 1u << 0,
+  /* C = round(gelu(acc + bias)), erf GELU: the GEMM followed by
+   * `audio_bias_gelu` (src/audio_encoder_gpu.rs:1594-1602, src/shaders.rs:2599)
+   * as one kernel.  Not combinable with QA_ACCUMULATE. */
+  QA_EPI_GELU = 1u << 1,
+  /* W holds n = 2*inter rows, [gate | up] (src/decoder.rs:1628-1634);
+   * C[:, j] = round(silu(round(g_j)) * round(u_j)) for j < n/2: the gate|up GEMM
+   * followed by `silu_mul_split` (src/decoder.rs:1636-1650) as one kernel.
+   * Not combinable with a bias, QA_ACCUMULATE, QA_EPI_GELU or QA_TRANSB. */
+  QA_EPI_SILU_MUL = 1u << 2,
+  /* W is read as [k, n] row-major (the conv GEMM's im2col operand,
+   * `gemm_conv`, src/audio_encoder_gpu.rs:1714-1721). */
+  QA_TRANSB = 1u << 3,
+  /* The bias is indexed by output ROW m instead of column: the channel-major
+   * conv activation, `audio_bias_gelu` mode 1 (src/shaders.rs:2636-2644,
+   * src/audio_encoder_gpu.rs:1777-1790).  Requires a bias. */
+  QA_BIAS_ROWS = 1u << 4
+};
+
+/* One projection C = A . W^T (+ epilogue).  Replaces a `GDims` uniform plus
+ * its bind group and dispatch (src/decoder.rs:1070-1104,
+ * src/audio_encoder_gpu.rs:1895-1944).
+ *
+ *   a    [m, k]  row stride lda            (the activations)
+ *   w    [n, k]  row stride ldb            (checkpoint [out, in] layout;
+ *                                           [k, n] under QA_TRANSB)
+ *   c    [m, n]  row stride ldc            ([m, n/2] under QA_EPI_SILU_MUL)
+ *   bias [n] or NULL                       (per output column; [m] per
+ *                                           output row under QA_BIAS_ROWS)
+ *   batch >= 1 independent problems, element offsets bsa/bsb/bsc apart
+ *   (the reference's wgid.z batch, src/shaders.rs:1870-1874).
+ *
+ * Requirements: k, lda, ldb multiples of 8 (16-byte rows, the reference pads
+ * k to 16, src/audio_encoder_gpu.rs:2266-2268); output columns and ldc
+ * multiples of 4; n a multiple of 8 under QA_TRANSB or QA_EPI_SILU_MUL;
+ * pointers 16-byte aligned (qa_alloc returns 256-byte aligned memory).
+ * m may be any value >= 0 (no padding to a tile multiple is needed, unlike
+ * the reference's `mp`, src/decoder.rs:907-910). */
+typedef struct qa_linear_desc {
+  uint32_t dtype; /* QA_F16 / QA_BF16 */
+  uint32_t flags; /* QA_ACCUMULATE | QA_EPI_* | QA_TRANSB */
+  int64_t m, n, k;
+  int64_t lda, ldb, ldc;
+  const void* a;
+  const void* w;
+  void* c;
+  const void* bias;
+  int64_t batch;
+  int64_t bsa, bsb, bsc;
+} qa_linear_desc;
+
+/* The decoder MLP block h += down(silu(x.Wg^T) * (x.Wu^T)): the gu GEMM,
+ * `silu_mul_split` and the down GEMM of src/decoder.rs:1628-1657 (CPU twin:
+ * src/cpu_decoder.rs:495-506).  `act` is caller-owned scratch (the reference's
+ * `activated` buffer); h may alias x (out = MLP(x) + x). */
+typedef struct qa_mlp_desc {
+  uint32_t dtype;
+  uint32_t flags;       /* reserved, must be 0 */
+  int64_t m, hidden, inter;
+  const void* x;        /* [m, hidden]                                 */
+  const void* w_gu;     /* [2*inter, hidden]: gate rows, then up rows  */
+  const void* w_down;   /* [hidden, inter]                             */
+  void* act;            /* [m, inter] scratch                          */
+  void* h;              /* [m, hidden] residual, updated in place      */
+} qa_mlp_desc;
+
+/* Context: device selection plus one in-order stream.  Replaces Gpu::new_with
+ * (src/gpu.rs:475-622) for this path.  Fails with QA_EDEVICE when no device is
+ * visible and QA_EUNSUPPORTED when the device is not gfx950. */
+int qa_ctx_create(int device, qa_ctx** out);
+int qa_ctx_destroy(qa_ctx* ctx);
+/* The context's hipStream_t, for callers that record events or capture
+ * graphs around qa_* launches (the reference exposes its queue the same way,
+ * `gpu.queue`). */
+void* qa_ctx_stream(qa_ctx* ctx);
+
+/* Device memory (Gpu::storage, src/gpu.rs:672-682: sizes padded to 16 B). */
+int qa_alloc(qa_ctx* ctx, size_t bytes, void** out);
+int qa_free(qa_ctx* ctx, void* ptr);
+/* Host -> device copy at byte offset `off`; the host bytes are consumed
+ * before return (Gpu::upload / write_at, src/gpu.rs:697-705). */
+int qa_upload(qa_ctx* ctx, void* dst, size_t off, const void* src, size_t bytes);
+/* Device -> host copy; waits for prior work (Gpu::readback, src/gpu.rs:735-762). */
+int qa_download(qa_ctx* ctx, void* dst, const void* src, size_t off, size_t bytes);
+/* Wait for every launch so far; reports asynchronous faults (Gpu::flush/pump,
+ * src/gpu.rs:709-728). */
+int qa_sync(qa_ctx* ctx);
+
+/* Launch one projection (see qa_linear_desc). */
+int qa_linear(qa_ctx* ctx, const qa_linear_desc* desc);
+/* Validate a descriptor without a device or a launch (the size guards of
+ * src/decoder.rs:927-950 and src/audio_encoder_gpu.rs:216-245). */
+int qa_linear_validate(const qa_linear_desc* desc);
+/* Launch the MLP block (see qa_mlp_desc). */
+int qa_mlp_fused(qa_ctx* ctx, const qa_mlp_desc* desc);
+
+/* Message of the last failure on this thread ("" if none). */
+const char* qa_last_error(void);
+/* Library version string, e.g. "qa 0.1.0 (abi 1, gfx950)". */
+const char* qa_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QA_H */

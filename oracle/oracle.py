@@ -1,0 +1,191 @@
+"""ctypes view of the CPU oracle (oracle/liboracle.so).
+
+TEST INFRASTRUCTURE ONLY.  Imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg, as the checker and as the timed CPU baseline.
+The product (libqa.so and its Python binding) never imports this module.
+
+Each wrapper names the C function it calls; the C file cites the reference
+(eclipse005/qwen3-aligner-wgpu) file:line every function restates.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+
+F16, BF16 = 0, 1
+ACCUMULATE, EPI_GELU, EPI_SILU_MUL, TRANSB, BIAS_ROWS, EXACT = 1, 2, 4, 8, 16, 256
+
+
+class LinearDesc(ctypes.Structure):
+    _fields_ = [
+        ("dtype", ctypes.c_uint32),
+        ("flags", ctypes.c_uint32),
+        ("m", ctypes.c_int64),
+        ("n", ctypes.c_int64),
+        ("k", ctypes.c_int64),
+        ("lda", ctypes.c_int64),
+        ("ldb", ctypes.c_int64),
+        ("ldc", ctypes.c_int64),
+        ("a", ctypes.c_void_p),
+        ("w", ctypes.c_void_p),
+        ("c", ctypes.c_void_p),
+        ("bias", ctypes.c_void_p),
+        ("batch", ctypes.c_int64),
+        ("bsa", ctypes.c_int64),
+        ("bsb", ctypes.c_int64),
+        ("bsc", ctypes.c_int64),
+    ]
+
+
+def build(force: bool = False) -> str:
+    """Compile liboracle.so with its Makefile (gcc + OpenMP)."""
+    import subprocess
+
+    cmd = ["make", "-C", _HERE] + (["-B"] if force else [])
+    subprocess.run(cmd, check=True, stdout=subprocess.DEVNULL)
+    return _LIB_PATH
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            raise RuntimeError(f"{_LIB_PATH} is not built; run oracle.build() or make -C oracle")
+        L = ctypes.CDLL(_LIB_PATH)
+        L.or_f16_from_f32.restype = ctypes.c_uint16
+        L.or_f16_from_f32.argtypes = [ctypes.c_float]
+        L.or_f16_to_f32.restype = ctypes.c_float
+        L.or_f16_to_f32.argtypes = [ctypes.c_uint16]
+        L.or_bf16_from_f32.restype = ctypes.c_uint16
+        L.or_bf16_from_f32.argtypes = [ctypes.c_float]
+        L.or_bf16_to_f32.restype = ctypes.c_float
+        L.or_bf16_to_f32.argtypes = [ctypes.c_uint16]
+        p = ctypes.c_void_p
+        i64 = ctypes.c_int64
+        L.or_h16_to_f32_n.argtypes = [p, p, i64, ctypes.c_int]
+        L.or_f32_to_h16_n.argtypes = [p, p, i64, ctypes.c_int]
+        L.or_gemm_f32.argtypes = [i64, i64, i64, p, i64, p, i64, p, i64, ctypes.c_float]
+        L.or_gemm_f32_naive.argtypes = [i64, i64, i64, p, i64, p, i64, p, i64]
+        L.or_gemm_f64.argtypes = [i64, i64, i64, p, i64, p, i64, p, i64]
+        L.or_silu_mul.restype = ctypes.c_float
+        L.or_silu_mul.argtypes = [ctypes.c_float, ctypes.c_float]
+        L.or_gelu.restype = ctypes.c_float
+        L.or_gelu.argtypes = [ctypes.c_float]
+        L.or_linear.restype = ctypes.c_int
+        L.or_linear.argtypes = [ctypes.POINTER(LinearDesc)]
+        L.or_num_threads.restype = ctypes.c_int
+        _lib = L
+    return _lib
+
+
+def _ptr(a: np.ndarray) -> int:
+    return a.ctypes.data
+
+
+def _c(a: np.ndarray, dtype) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+def h16_from_f32(x: np.ndarray, dtype: int) -> np.ndarray:
+    """or_f32_to_h16_n: f32 -> 16-bit bits (uint16) in `dtype`'s format."""
+    x = _c(x, np.float32)
+    out = np.empty(x.shape, np.uint16)
+    lib().or_f32_to_h16_n(_ptr(x), _ptr(out), x.size, dtype)
+    return out
+
+
+def h16_to_f32(h: np.ndarray, dtype: int) -> np.ndarray:
+    """or_h16_to_f32_n: 16-bit bits -> f32 values (exact)."""
+    h = _c(h, np.uint16)
+    out = np.empty(h.shape, np.float32)
+    lib().or_h16_to_f32_n(_ptr(h), _ptr(out), h.size, dtype)
+    return out
+
+
+def gemm_f32(x: np.ndarray, w: np.ndarray, out: np.ndarray | None = None, beta: float = 0.0) -> np.ndarray:
+    """or_gemm_f32: out = beta*out + x @ w.T (x [m,k], w [n,k], f32)."""
+    x = _c(x, np.float32)
+    w = _c(w, np.float32)
+    m, k = x.shape
+    n = w.shape[0]
+    assert w.shape[1] == k
+    if out is None:
+        out = np.zeros((m, n), np.float32)
+    assert out.dtype == np.float32 and out.flags.c_contiguous and out.shape == (m, n)
+    lib().or_gemm_f32(m, n, k, _ptr(x), k, _ptr(w), k, _ptr(out), n, beta)
+    return out
+
+
+def gemm_f32_naive(x: np.ndarray, w: np.ndarray) -> np.ndarray:
+    """or_gemm_f32_naive: sequential f32 triple loop."""
+    x = _c(x, np.float32)
+    w = _c(w, np.float32)
+    m, k = x.shape
+    n = w.shape[0]
+    out = np.empty((m, n), np.float32)
+    lib().or_gemm_f32_naive(m, n, k, _ptr(x), k, _ptr(w), k, _ptr(out), n)
+    return out
+
+
+def gemm_f64(x: np.ndarray, w: np.ndarray) -> np.ndarray:
+    """or_gemm_f64: f64 triple loop over f32 inputs."""
+    x = _c(x, np.float32)
+    w = _c(w, np.float32)
+    m, k = x.shape
+    n = w.shape[0]
+    out = np.empty((m, n), np.float64)
+    lib().or_gemm_f64(m, n, k, _ptr(x), k, _ptr(w), k, _ptr(out), n)
+    return out
+
+
+def silu_mul(g: float, u: float) -> float:
+    return lib().or_silu_mul(g, u)
+
+
+def gelu(x: float) -> float:
+    return lib().or_gelu(x)
+
+
+def linear(dtype: int, a: np.ndarray, w: np.ndarray, c: np.ndarray, *, flags: int = 0,
+           bias: np.ndarray | None = None, m: int | None = None, n: int | None = None,
+           k: int | None = None, lda: int | None = None, ldb: int | None = None,
+           ldc: int | None = None, batch: int = 1, bsa: int = 0, bsb: int = 0,
+           bsc: int = 0) -> np.ndarray:
+    """or_linear on uint16 bit arrays; updates and returns `c`.
+
+    Shapes default from the arrays: a [m,k], w [n,k] ([k,n] with TRANSB),
+    c [m, n] ([m, n/2] with EPI_SILU_MUL)."""
+    for arr in (a, w, c):
+        assert arr.dtype == np.uint16 and arr.flags.c_contiguous
+    if bias is not None:
+        assert bias.dtype == np.uint16 and bias.flags.c_contiguous
+    if m is None:
+        m = a.shape[-2]
+    if k is None:
+        k = a.shape[-1]
+    if n is None:
+        n = w.shape[-1] if flags & TRANSB else w.shape[-2]
+    d = LinearDesc(
+        dtype=dtype, flags=flags, m=m, n=n, k=k,
+        lda=lda if lda is not None else a.shape[-1],
+        ldb=ldb if ldb is not None else w.shape[-1],
+        ldc=ldc if ldc is not None else c.shape[-1],
+        a=_ptr(a), w=_ptr(w), c=_ptr(c), bias=_ptr(bias) if bias is not None else None,
+        batch=batch, bsa=bsa, bsb=bsb, bsc=bsc,
+    )
+    rc = lib().or_linear(ctypes.byref(d))
+    if rc != 0:
+        raise ValueError(f"or_linear rejected the descriptor (rc={rc})")
+    return c
+
+
+def num_threads() -> int:
+    return lib().or_num_threads()

@@ -1,0 +1,101 @@
+/*
+ * qa_oracle.h -- CPU restatement of the reference's linear-layer path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Nothing in the product (libqa.so, the host mirror,
+ * the Python binding) links, loads or calls this code.  Only tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg use it, and only as
+ * the checker / the timed CPU baseline, never as the thing measured on the GPU.
+ *
+ * What it restates (reference = eclipse005/qwen3-aligner-wgpu):
+ *   - 16-bit storage formats and their rounding:
+ *       f16  : IEEE binary16 round-to-nearest-even, as half 2.7.1's
+ *              f16::from_f32 used by src/cpu_decoder.rs:68,89 and
+ *              src/half16.rs:40-47.
+ *       bf16 : src/shaders.rs:169-179 rne_bf16_bits,
+ *              (u + 0x7FFF + ((u >> 16) & 1)) >> 16.
+ *   - the f32 GEMM out = beta*out + x.W^T of the gemm crate 0.18.2 wrapper
+ *     gemm_row_major (src/cpu_decoder.rs:583-610, src/cpu_tensor.rs:82-108).
+ *   - the linear op with one rounding per output (src/shaders.rs:2045-2073,
+ *     src/cpu_decoder.rs:59-97), the SiLU.up loop (src/cpu_decoder.rs:496-505)
+ *     and the erf-form GELU (src/audio_encoder.rs:196-202).
+ *
+ * Parity pins (each function is checked in tests/test_oracle.py):
+ *   or_f16_from_f32  : numpy float32->float16 cast over the reference's
+ *                      halfway grid + 500k LCG sweep (src/shaders.rs:191-243).
+ *   or_bf16_from_f32 : KAT 0.1 -> 0x3DCD (src/half16.rs:113-119); torch's
+ *                      float32->bfloat16 cast over the same grid and sweep.
+ *   or_gemm_f32      : the reference KAT gemm_row_major_matches_naive
+ *                      (src/cpu_decoder.rs:620-646, worst |d| < 1e-3) and
+ *                      numpy float64 matmul.
+ *   or_gemm_f64      : numpy float64 matmul (to 1e-12 relative).
+ *   or_linear        : invariants (zero A keeps C, bias-only, fused-row
+ *                      splits), f64 closed forms, SiLU brute force over all
+ *                      65536 f16 gate values, GELU against math.erf.
+ */
+#ifndef QA_ORACLE_H
+#define QA_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { OR_F16 = 0, OR_BF16 = 1 };
+enum {
+  OR_ACCUMULATE = 1u << 0,
+  OR_EPI_GELU = 1u << 1,
+  OR_EPI_SILU_MUL = 1u << 2,
+  OR_TRANSB = 1u << 3,
+  OR_BIAS_ROWS = 1u << 4,
+  OR_EXACT = 1u << 8, /* accumulate in f64 instead of the blocked f32 GEMM */
+};
+
+uint16_t or_f16_from_f32(float x);
+float or_f16_to_f32(uint16_t h);
+uint16_t or_bf16_from_f32(float x);
+float or_bf16_to_f32(uint16_t h);
+uint16_t or_h16_from_f32(float x, int dtype);
+float or_h16_to_f32(uint16_t h, int dtype);
+
+/* Bulk conversions (n elements). */
+void or_h16_to_f32_n(const uint16_t* src, float* dst, int64_t n, int dtype);
+void or_f32_to_h16_n(const float* src, uint16_t* dst, int64_t n, int dtype);
+
+/* out[i*ldo+j] = beta*out[i*ldo+j] + sum_p x[i*ldx+p]*w[j*ldw+p]
+ * (out is only read when beta != 0, as the gemm crate's read_dst flag). */
+void or_gemm_f32(int64_t m, int64_t n, int64_t k, const float* x, int64_t ldx,
+                 const float* w, int64_t ldw, float* out, int64_t ldo, float beta);
+/* Sequential f32 triple loop -- the naive side of the reference KAT. */
+void or_gemm_f32_naive(int64_t m, int64_t n, int64_t k, const float* x, int64_t ldx,
+                       const float* w, int64_t ldw, float* out, int64_t ldo);
+/* f64 triple loop over f32 inputs: the exact-value pin. */
+void or_gemm_f64(int64_t m, int64_t n, int64_t k, const float* x, int64_t ldx,
+                 const float* w, int64_t ldw, double* out, int64_t ldo);
+
+float or_silu_mul(float g, float u); /* g/(1+exp(-g)) * u, f32 */
+float or_gelu(float x);              /* 0.5x(1+erf(x/sqrt2)), f32 */
+
+/* The linear op, same fields and meaning as qa_linear_desc (include/qa.h). */
+typedef struct or_linear_desc {
+  uint32_t dtype;
+  uint32_t flags;
+  int64_t m, n, k;
+  int64_t lda, ldb, ldc;
+  const uint16_t* a;
+  const uint16_t* w;
+  uint16_t* c;
+  const uint16_t* bias;
+  int64_t batch, bsa, bsb, bsc;
+} or_linear_desc;
+
+/* Returns 0 on success, -1 on an invalid descriptor. */
+int or_linear(const or_linear_desc* d);
+
+/* Number of OpenMP threads the oracle's parallel loops use. */
+int or_num_threads(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

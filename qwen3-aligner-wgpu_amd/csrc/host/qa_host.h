@@ -1,0 +1,116 @@
+/*
+ * qa_host.h -- C surface of the C++ host mirror (linear_sites.cpp) for the
+ * Python harness (tests, bench, smoke).
+ *
+ * The mirror re-creates, on top of the C ABI in include/qa.h only, what the
+ * reference's Rust host does around its GEMM dispatches:
+ *   - the text decoder's per-layer projections of WgpuTextDecoder::prefill
+ *     (src/decoder.rs:1321-1327 qkv, :1602-1608 o + residual, :1628-1650
+ *     gate|up + SiLU, :1652-1657 down + residual) over the fused
+ *     [q|k|v] / [gate|up] weights of convert_layer / fused_pieces
+ *     (src/decoder.rs:816-871);
+ *   - the audio tower's linears of GpuAudioEncoder::layer
+ *     (src/audio_encoder_gpu.rs:1414-1419 qkv + bias, :1579-1581 o + bias +
+ *     residual, :1594-1602 fc1 + bias + GELU, :1603-1605 fc2 + bias + residual)
+ *     and a conv block as an im2col GEMM + bias + GELU
+ *     (src/audio_encoder.rs:376-447, the CPU conv block).
+ * The non-GEMM ops between them (norms, attention, RoPE) are not part of this
+ * path; their outputs are fixed synthetic inputs here.
+ *
+ * It is not part of the product boundary (include/qa.h): a Rust caller keeps
+ * its own host code and binds only include/qa.h.
+ */
+#ifndef QA_HOST_H
+#define QA_HOST_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "qa.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Seeded synthetic values: SplitMix64 counter stream salted by tensor id,
+ * Box-Muller in f64, mean + std*z rounded to f32 then RNE to the 16-bit
+ * format.  Deterministic for any thread count. */
+void qah_synth_normal_h16(uint64_t seed, uint64_t tensor_id, float mean, float std_dev,
+                          int dtype, uint16_t* out, size_t n);
+/* Same stream, as f32 values (no 16-bit rounding). */
+void qah_synth_normal_f32(uint64_t seed, uint64_t tensor_id, float mean, float std_dev,
+                          float* out, size_t n);
+/* f32 -> 16-bit RNE narrowing (weights.rs narrow_h16_into, src/weights.rs:57-89). */
+void qah_narrow_f32(const float* src, uint16_t* dst, size_t n, int dtype);
+/* Rows [rows, cols] of `parts` concatenated along the output dimension
+ * (PackedWeight::concat_rows, src/weights.rs:345-360; fused_pieces,
+ * src/decoder.rs:840-871). */
+void qah_concat_rows(const uint16_t* const* parts, const int64_t* rows, int nparts, int64_t cols,
+                     uint16_t* dst);
+
+/* ---- text decoder projections ---- */
+typedef struct qah_decoder qah_decoder;
+int qah_decoder_create(qa_ctx* ctx, int dtype, int layers, int hidden, int q_dim, int kv_dim,
+                       int inter, int max_rows, qah_decoder** out);
+/* Uploads layer `li`'s weights, each row-major [out, in]; q|k|v and gate|up
+ * are fused into one matrix each, as the reference uploads them. */
+int qah_decoder_load_layer(qah_decoder* d, int li, const uint16_t* q, const uint16_t* k,
+                           const uint16_t* v, const uint16_t* o, const uint16_t* gate,
+                           const uint16_t* up, const uint16_t* down);
+/* The non-GEMM ops' outputs the projections read: normed [rows, hidden]
+ * (input RMSNorm), attn [rows, q_dim] (attention), norm2 [rows, hidden]
+ * (post-attention RMSNorm), and the residual stream h [rows, hidden]. */
+int qah_decoder_set_inputs(qah_decoder* d, int rows, const uint16_t* normed,
+                           const uint16_t* attn, const uint16_t* norm2, const uint16_t* h);
+/* Enqueue every layer's four projections (no wait). */
+int qah_decoder_prefill_linears(qah_decoder* d, int rows);
+/* Copy back: which = 0 h [rows, hidden], 1 qkv [rows, q+2kv] of the last
+ * layer run, 2 act [rows, inter] of the last layer run. */
+int qah_decoder_read(qah_decoder* d, int which, int rows, uint16_t* host);
+/* Time `steps` forward passes after `warmup` (HIP events on the context's
+ * stream).  use_graph = 1 replays one captured hipGraph per step. */
+int qah_decoder_time(qah_decoder* d, int rows, int warmup, int steps, int use_graph,
+                     double* ms_per_step);
+/* Per-site average kernel duration (ms) over `steps` passes, each launch
+ * bracketed by its own pair of HIP events: site_ms[0..3] = qkv, o, gu, down. */
+int qah_decoder_profile_sites(qah_decoder* d, int rows, int steps, double* site_ms);
+void qah_decoder_destroy(qah_decoder* d);
+
+/* ---- audio tower linears ---- */
+typedef struct qah_encoder qah_encoder;
+int qah_encoder_create(qa_ctx* ctx, int dtype, int layers, int d_model, int ffn, int conv_k,
+                       int max_rows, qah_encoder** out);
+/* Layer li: qkv_w [3d, d] (fused q|k|v rows, src/audio_encoder_gpu.rs:292-313)
+ * with qkv_b [3d]; o_w [d, d], o_b [d]; fc1_w [ffn, d], fc1_b [ffn];
+ * fc2_w [d, ffn], fc2_b [d]. */
+int qah_encoder_load_layer(qah_encoder* e, int li, const uint16_t* qkv_w, const uint16_t* qkv_b,
+                           const uint16_t* o_w, const uint16_t* o_b, const uint16_t* fc1_w,
+                           const uint16_t* fc1_b, const uint16_t* fc2_w, const uint16_t* fc2_b);
+/* The conv block as a GEMM: w [d, conv_k] (conv weight flattened to im2col k
+ * order, src/audio_encoder_gpu.rs:262-285), b [d]. */
+int qah_encoder_load_conv(qah_encoder* e, const uint16_t* w, const uint16_t* b);
+/* col [rows, conv_k] im2col operand; normed [rows, d] (LayerNorm 1 output);
+ * attn [rows, d] (attention output); norm2 [rows, d] (LayerNorm 2 output);
+ * h [rows, d] residual stream. */
+int qah_encoder_set_inputs(qah_encoder* e, int rows, const uint16_t* col, const uint16_t* normed,
+                           const uint16_t* attn, const uint16_t* norm2, const uint16_t* h);
+/* conv GEMM (+bias+GELU) into `conv_out`, then every layer's 4 linears. */
+int qah_encoder_forward_linears(qah_encoder* e, int rows);
+/* which = 0 h [rows, d], 1 conv_out [rows, d], 2 qkv [rows, 3d] and
+ * 3 act [rows, ffn] of the last layer run. */
+int qah_encoder_read(qah_encoder* e, int which, int rows, uint16_t* host);
+int qah_encoder_time(qah_encoder* e, int rows, int warmup, int steps, int use_graph,
+                     double* ms_per_step);
+/* site_ms[0..4] = conv, qkv, o, fc1, fc2 */
+int qah_encoder_profile_sites(qah_encoder* e, int rows, int steps, double* site_ms);
+void qah_encoder_destroy(qah_encoder* e);
+
+/* Time `iters` back-to-back launches of one descriptor (HIP events around the
+ * whole run on the context's stream); ms per launch. */
+int qah_time_linear(qa_ctx* ctx, const qa_linear_desc* desc, int warmup, int iters,
+                    double* ms_per_launch);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

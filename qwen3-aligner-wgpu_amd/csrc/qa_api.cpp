@@ -1,0 +1,393 @@
+// qa_api.cpp -- the C ABI of include/qa.h over HIP.
+//
+// Replaces, for the linear-layer path, the reference's wgpu device runtime
+// (src/gpu.rs: storage/upload/readback/flush, :672-762) and the GEMM dispatch
+// helpers (src/decoder.rs:1030-1104, src/audio_encoder_gpu.rs:1895-1944).
+// There is no pipeline compile or cache (src/gpu.rs:774-890): the kernels are
+// gfx950 code objects linked into this library.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+
+#include "qa.h"
+#include "qa_internal.h"
+
+struct qa_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  int num_cus = 256;
+  float* ws = nullptr;  // split-K partials
+  size_t ws_floats = 0;
+};
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int ok() { return QA_OK; }
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(e == hipErrorOutOfMemory ? QA_ENOMEM : QA_EDEVICE, "%s: %s (%d)", what,
+              hipGetErrorString(e), (int)e);
+}
+
+bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+constexpr uint32_t kKnownFlags =
+    QA_ACCUMULATE | QA_EPI_GELU | QA_EPI_SILU_MUL | QA_TRANSB | QA_BIAS_ROWS;
+constexpr int64_t kI32 = 0x7fffffff;
+
+// Byte span [lo, hi) an operand covers over all batches.
+struct Span {
+  uintptr_t lo, hi;
+};
+Span span_of(const void* p, int64_t rows, int64_t cols, int64_t ld, int64_t batch, int64_t bs) {
+  const uintptr_t lo = (uintptr_t)p;
+  const int64_t last = (batch - 1) * bs + (rows - 1) * ld + cols;  // elements
+  return {lo, lo + (uintptr_t)(last * 2)};
+}
+bool overlap(Span a, Span b) { return a.lo < b.hi && b.lo < a.hi; }
+
+int validate(const qa_linear_desc* d) {
+  if (!d) return fail(QA_EINVAL, "qa_linear: null descriptor");
+  if (d->dtype != QA_F16 && d->dtype != QA_BF16)
+    return fail(QA_EINVAL, "qa_linear: dtype %u is neither QA_F16 nor QA_BF16", d->dtype);
+  if (d->flags & ~kKnownFlags) return fail(QA_EINVAL, "qa_linear: unknown flags 0x%x", d->flags);
+  const bool silu = d->flags & QA_EPI_SILU_MUL, gelu = d->flags & QA_EPI_GELU;
+  const bool accum = d->flags & QA_ACCUMULATE, transb = d->flags & QA_TRANSB;
+  const bool brow = d->flags & QA_BIAS_ROWS;
+  if (d->m < 0 || d->n <= 0 || d->k <= 0)
+    return fail(QA_EINVAL, "qa_linear: bad shape m=%lld n=%lld k=%lld", (long long)d->m,
+                (long long)d->n, (long long)d->k);
+  if (d->m > kI32 || d->n > kI32 || d->k > kI32 || d->lda > kI32 || d->ldb > kI32 ||
+      d->ldc > kI32)
+    return fail(QA_EINVAL, "qa_linear: dimensions and strides must be below 2^31");
+  if (!d->a || !d->w || !d->c) return fail(QA_EINVAL, "qa_linear: null operand pointer");
+  if (d->k % 8) return fail(QA_EINVAL, "qa_linear: k=%lld is not a multiple of 8", (long long)d->k);
+  if (d->lda < d->k || d->lda % 8)
+    return fail(QA_EINVAL, "qa_linear: lda=%lld must be >= k and a multiple of 8",
+                (long long)d->lda);
+  if (silu && (gelu || accum || transb || brow || d->bias))
+    return fail(QA_EINVAL, "qa_linear: QA_EPI_SILU_MUL takes no bias, residual, GELU or TRANSB");
+  if (gelu && accum) return fail(QA_EINVAL, "qa_linear: QA_EPI_GELU with QA_ACCUMULATE");
+  if (brow && !d->bias) return fail(QA_EINVAL, "qa_linear: QA_BIAS_ROWS without a bias");
+  if (silu && d->n % 8)
+    return fail(QA_EINVAL, "qa_linear: SiLU-mul needs n (= 2*inter) a multiple of 8, got %lld",
+                (long long)d->n);
+  if (transb) {
+    if (d->n % 8) return fail(QA_EINVAL, "qa_linear: TRANSB needs n a multiple of 8");
+    if (d->ldb < d->n || d->ldb % 8)
+      return fail(QA_EINVAL, "qa_linear: TRANSB needs ldb >= n and a multiple of 8");
+  } else if (d->ldb < d->k || d->ldb % 8) {
+    return fail(QA_EINVAL, "qa_linear: ldb=%lld must be >= k and a multiple of 8",
+                (long long)d->ldb);
+  }
+  const int64_t nout = silu ? d->n / 2 : d->n;
+  if (nout % 4) return fail(QA_EINVAL, "qa_linear: output columns %lld not a multiple of 4",
+                            (long long)nout);
+  if (d->ldc < nout || d->ldc % 4)
+    return fail(QA_EINVAL, "qa_linear: ldc=%lld must be >= %lld and a multiple of 4",
+                (long long)d->ldc, (long long)nout);
+  const int64_t batch = d->batch > 0 ? d->batch : 1;
+  if (batch > 65535) return fail(QA_EINVAL, "qa_linear: batch %lld > 65535", (long long)batch);
+  if (batch > 1) {
+    if (d->bsa < 0 || d->bsb < 0 || d->bsc < 0 || d->bsa % 8 || d->bsb % 8 || d->bsc % 4)
+      return fail(QA_EINVAL,
+                  "qa_linear: batch strides must be >= 0, bsa/bsb multiples of 8, bsc of 4");
+  }
+  if (!aligned(d->a, 16) || !aligned(d->w, 16))
+    return fail(QA_EINVAL, "qa_linear: a and w must be 16-byte aligned");
+  if (!aligned(d->c, 8) || (d->bias && !aligned(d->bias, 8)))
+    return fail(QA_EINVAL, "qa_linear: c and bias must be 8-byte aligned");
+  if (((d->m > 0 ? d->m - 1 : 0) * d->lda + d->k) * 2 >= (int64_t)1 << 31 ||
+      (((transb ? d->k : d->n) - 1) * d->ldb + (transb ? d->n : d->k)) * 2 >= (int64_t)1 << 31)
+    return fail(QA_EUNSUPPORTED, "qa_linear: an operand spans 2 GiB or more (one batch)");
+  if (d->m > 0) {
+    const Span sa = span_of(d->a, d->m, d->k, d->lda, batch, d->bsa);
+    const Span sw = transb ? span_of(d->w, d->k, d->n, d->ldb, batch, d->bsb)
+                           : span_of(d->w, d->n, d->k, d->ldb, batch, d->bsb);
+    const Span sc = span_of(d->c, d->m, nout, d->ldc, batch, d->bsc);
+    if (overlap(sa, sc) || overlap(sw, sc))
+      return fail(QA_EINVAL, "qa_linear: c overlaps an input operand");
+  }
+  return ok();
+}
+
+// Tile / split-K choice.  Units (tiles x splits) should cover the CUs at
+// least once; among tile shapes, prefer the one with the fewest "rounds" of
+// work per CU, measured in 128x128x64 MFMA-stage equivalents, then the
+// larger tile (fewer operand bytes per flop).
+qa::Plan plan_linear(const qa_linear_desc& d, int num_cus) {
+  qa::Plan pl{};
+  const bool silu = d.flags & QA_EPI_SILU_MUL;
+  pl.epi = silu ? qa::EPI_SILU : (d.flags & QA_EPI_GELU) ? qa::EPI_GELU : qa::EPI_PLAIN;
+  pl.transb = (d.flags & QA_TRANSB) != 0;
+  const int64_t M = d.m, N = d.n, K = d.k;
+  const int64_t nout = silu ? N / 2 : N;
+
+  int forced_tile = -1, forced_splits = 0;
+  if (const char* e = getenv("QA_TILE")) forced_tile = atoi(e);
+  if (const char* e = getenv("QA_SPLITS")) forced_splits = atoi(e);
+
+  int cands[qa::TILE_COUNT] = {qa::TILE_128x128, qa::TILE_256x128, qa::TILE_128x256,
+                               qa::TILE_64x128};
+  int ncand = qa::TILE_COUNT;
+  if (pl.transb) ncand = 1;  // the conv operand path has one tile shape
+  if (forced_tile >= 0 && forced_tile < qa::TILE_COUNT && !pl.transb) {
+    cands[0] = forced_tile;
+    ncand = 1;
+  }
+  double best = 1e300;
+  for (int ci = 0; ci < ncand; ++ci) {
+    const qa::TileShape ts = qa::tile_shape(cands[ci]);
+    const int64_t tbn = silu ? ts.bn / 2 : ts.bn;
+    const int64_t tm = (M + ts.bm - 1) / ts.bm, tn = (nout + tbn - 1) / tbn;
+    const int64_t tiles = tm * tn;
+    int64_t splits = 1;
+    if (forced_splits > 0) {
+      splits = forced_splits;
+    } else {
+      // Split K while the units leave at least a quarter of the CUs idle and
+      // each split keeps >= 256 of k (4 LDS stages).
+      while (tiles * splits * 4 < (int64_t)num_cus * 3 && K / (splits * 2) >= 256) splits *= 2;
+    }
+    int64_t kchunk = ((K + splits - 1) / splits + 63) / 64 * 64;
+    splits = (K + kchunk - 1) / kchunk;
+    const int64_t units = tiles * splits;
+    const int64_t rounds = (units + num_cus - 1) / num_cus;
+    // Per-unit cost in 128x128x64 stage equivalents, plus a fixed overhead
+    // per unit (prologue + epilogue ~ 2 stages) and per split (partials).
+    const double stages = (double)kchunk / 64.0;
+    const double area = (double)ts.bm * ts.bn / (128.0 * 128.0);
+    const double eff = (ts.bm * ts.bn >= 256 * 128) ? 0.9 : (ts.bm * ts.bn <= 64 * 128 ? 1.25 : 1.0);
+    const double cost = (double)rounds * (area * eff * stages + 2.0 + (splits > 1 ? 1.0 : 0.0));
+    if (cost < best * 0.999) {
+      best = cost;
+      pl.tile = cands[ci];
+      pl.tiles_m = (int)tm;
+      pl.tiles_n = (int)tn;
+      pl.splits = (int)splits;
+      pl.kchunk = (int)kchunk;
+    }
+  }
+  if (pl.splits > 1) pl.ws_floats = (size_t)pl.splits * (size_t)M * (size_t)N;
+  return pl;
+}
+
+int ensure_workspace(qa_ctx* ctx, size_t floats) {
+  if (floats <= ctx->ws_floats) return ok();
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(ctx->stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+    return fail(QA_EINVAL,
+                "qa_linear: the split-K workspace must grow (%zu floats) but the stream is "
+                "being captured; run the same call once before capture",
+                floats);
+  hipError_t e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+  if (ctx->ws) (void)hipFree(ctx->ws);
+  ctx->ws = nullptr;
+  ctx->ws_floats = 0;
+  e = hipMalloc(&ctx->ws, floats * sizeof(float));
+  if (e != hipSuccess) return hip_fail(e, "hipMalloc(split-K workspace)");
+  ctx->ws_floats = floats;
+  return ok();
+}
+
+int set_device(qa_ctx* ctx) {
+  const hipError_t e = hipSetDevice(ctx->device);
+  return e == hipSuccess ? ok() : hip_fail(e, "hipSetDevice");
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* qa_last_error(void) { return g_err.c_str(); }
+
+const char* qa_version(void) { return "qa 0.1.0 (abi 1, gfx950)"; }
+
+int qa_ctx_create(int device, qa_ctx** out) {
+  if (!out) return fail(QA_EINVAL, "qa_ctx_create: null output pointer");
+  *out = nullptr;
+  int count = 0;
+  hipError_t e = hipGetDeviceCount(&count);
+  if (e != hipSuccess || count <= 0)
+    return fail(QA_EDEVICE, "qa_ctx_create: no HIP device visible (%s)",
+                e == hipSuccess ? "device count 0" : hipGetErrorString(e));
+  if (device < 0 || device >= count)
+    return fail(QA_EINVAL, "qa_ctx_create: device %d out of range [0, %d)", device, count);
+  hipDeviceProp_t prop;
+  e = hipGetDeviceProperties(&prop, device);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDeviceProperties");
+  if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return fail(QA_EUNSUPPORTED, "qa_ctx_create: device %d is %s; this library runs on gfx950",
+                device, prop.gcnArchName);
+  e = hipSetDevice(device);
+  if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
+  qa_ctx* ctx = new qa_ctx;
+  ctx->device = device;
+  ctx->num_cus = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
+  e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    delete ctx;
+    return hip_fail(e, "hipStreamCreateWithFlags");
+  }
+  *out = ctx;
+  return ok();
+}
+
+int qa_ctx_destroy(qa_ctx* ctx) {
+  if (!ctx) return ok();
+  (void)hipSetDevice(ctx->device);
+  (void)hipStreamSynchronize(ctx->stream);
+  if (ctx->ws) (void)hipFree(ctx->ws);
+  const hipError_t e = hipStreamDestroy(ctx->stream);
+  delete ctx;
+  return e == hipSuccess ? ok() : hip_fail(e, "hipStreamDestroy");
+}
+
+void* qa_ctx_stream(qa_ctx* ctx) { return ctx ? (void*)ctx->stream : nullptr; }
+
+int qa_alloc(qa_ctx* ctx, size_t bytes, void** out) {
+  if (!ctx || !out) return fail(QA_EINVAL, "qa_alloc: null argument");
+  *out = nullptr;
+  if (int rc = set_device(ctx)) return rc;
+  const size_t padded = std::max<size_t>(16, (bytes + 15) & ~(size_t)15);
+  void* p = nullptr;
+  const hipError_t e = hipMalloc(&p, padded);
+  if (e != hipSuccess) return hip_fail(e, "hipMalloc");
+  *out = p;
+  return ok();
+}
+
+int qa_free(qa_ctx* ctx, void* ptr) {
+  if (!ctx) return fail(QA_EINVAL, "qa_free: null context");
+  if (!ptr) return ok();
+  if (int rc = set_device(ctx)) return rc;
+  const hipError_t e = hipFree(ptr);
+  return e == hipSuccess ? ok() : hip_fail(e, "hipFree");
+}
+
+int qa_upload(qa_ctx* ctx, void* dst, size_t off, const void* src, size_t bytes) {
+  if (!ctx || !dst || (!src && bytes)) return fail(QA_EINVAL, "qa_upload: null argument");
+  if (!bytes) return ok();
+  if (int rc = set_device(ctx)) return rc;
+  hipError_t e = hipMemcpyAsync((char*)dst + off, src, bytes, hipMemcpyHostToDevice, ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(H2D)");
+  e = hipStreamSynchronize(ctx->stream);
+  return e == hipSuccess ? ok() : hip_fail(e, "hipStreamSynchronize");
+}
+
+int qa_download(qa_ctx* ctx, void* dst, const void* src, size_t off, size_t bytes) {
+  if (!ctx || !src || (!dst && bytes)) return fail(QA_EINVAL, "qa_download: null argument");
+  if (!bytes) return ok();
+  if (int rc = set_device(ctx)) return rc;
+  hipError_t e =
+      hipMemcpyAsync(dst, (const char*)src + off, bytes, hipMemcpyDeviceToHost, ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(D2H)");
+  e = hipStreamSynchronize(ctx->stream);
+  return e == hipSuccess ? ok() : hip_fail(e, "hipStreamSynchronize");
+}
+
+int qa_sync(qa_ctx* ctx) {
+  if (!ctx) return fail(QA_EINVAL, "qa_sync: null context");
+  if (int rc = set_device(ctx)) return rc;
+  const hipError_t e = hipStreamSynchronize(ctx->stream);
+  return e == hipSuccess ? ok() : hip_fail(e, "qa_sync");
+}
+
+int qa_linear_validate(const qa_linear_desc* desc) { return validate(desc); }
+
+int qa_linear(qa_ctx* ctx, const qa_linear_desc* d) {
+  if (!ctx) return fail(QA_EINVAL, "qa_linear: null context");
+  if (int rc = validate(d)) return rc;
+  if (d->m == 0) return ok();
+  if (int rc = set_device(ctx)) return rc;
+  const qa::Plan plan = plan_linear(*d, ctx->num_cus);
+  if (plan.splits > 1) {
+    if (int rc = ensure_workspace(ctx, plan.ws_floats)) return rc;
+  }
+  qa::GemmParams p{};
+  p.a = (const uint16_t*)d->a;
+  p.w = (const uint16_t*)d->w;
+  p.c = (uint16_t*)d->c;
+  p.bias = (const uint16_t*)d->bias;
+  p.ws = ctx->ws;
+  p.a_bytes = (int)(((d->m - 1) * d->lda + d->k) * 2);
+  p.w_bytes = (int)((((d->flags & QA_TRANSB) ? d->k : d->n) - 1) * d->ldb +
+                    ((d->flags & QA_TRANSB) ? d->n : d->k)) * 2;
+  p.M = (int)d->m;
+  p.N = (int)d->n;
+  p.K = (int)d->k;
+  p.lda = (int)d->lda;
+  p.ldb = (int)d->ldb;
+  p.ldc = (int)d->ldc;
+  p.bsa = d->bsa;
+  p.bsb = d->bsb;
+  p.bsc = d->bsc;
+  p.tiles_m = plan.tiles_m;
+  p.tiles_n = plan.tiles_n;
+  p.splits = plan.splits;
+  p.kchunk = plan.kchunk;
+  p.accumulate = (d->flags & QA_ACCUMULATE) ? 1 : 0;
+  p.bias_rows = (d->flags & QA_BIAS_ROWS) ? 1 : 0;
+  const int batch = d->batch > 0 ? (int)d->batch : 1;
+  if (plan.splits > 1 && batch > 1)
+    return fail(QA_EUNSUPPORTED, "qa_linear: split-K with batch > 1");
+  const hipError_t e = qa::launch_gemm((int)d->dtype, plan, p, batch, ctx->stream);
+  return e == hipSuccess ? ok() : hip_fail(e, "qa_linear launch");
+}
+
+int qa_mlp_fused(qa_ctx* ctx, const qa_mlp_desc* d) {
+  if (!ctx || !d) return fail(QA_EINVAL, "qa_mlp_fused: null argument");
+  if (d->flags) return fail(QA_EINVAL, "qa_mlp_fused: flags must be 0");
+  if (d->m < 0 || d->hidden <= 0 || d->inter <= 0)
+    return fail(QA_EINVAL, "qa_mlp_fused: bad shape");
+  qa_linear_desc gu{};
+  gu.dtype = d->dtype;
+  gu.flags = QA_EPI_SILU_MUL;
+  gu.m = d->m;
+  gu.n = 2 * d->inter;
+  gu.k = d->hidden;
+  gu.lda = d->hidden;
+  gu.ldb = d->hidden;
+  gu.ldc = d->inter;
+  gu.a = d->x;
+  gu.w = d->w_gu;
+  gu.c = d->act;
+  gu.batch = 1;
+  qa_linear_desc down{};
+  down.dtype = d->dtype;
+  down.flags = QA_ACCUMULATE;
+  down.m = d->m;
+  down.n = d->hidden;
+  down.k = d->inter;
+  down.lda = d->inter;
+  down.ldb = d->inter;
+  down.ldc = d->hidden;
+  down.a = d->act;
+  down.w = d->w_down;
+  down.c = d->h;
+  down.batch = 1;
+  if (int rc = validate(&gu)) return rc;
+  if (int rc = validate(&down)) return rc;
+  if (int rc = qa_linear(ctx, &gu)) return rc;
+  return qa_linear(ctx, &down);
+}
+
+}  // extern "C"

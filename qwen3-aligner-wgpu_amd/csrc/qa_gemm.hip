@@ -1,0 +1,679 @@
+// qa_gemm.hip -- MFMA GEMM kernels for gfx950 (CDNA4): C = A . W^T + epilogue.
+//
+// The reference's WGSL `prefill_gemm` (src/shaders.rs:1846-2077) runs this
+// contraction as scalar f32 FMAs over a 128x128 tile with f32 LDS; here the
+// same contraction runs on the wave64 matrix cores.
+//
+// Main kernel (gemm_dma_kernel), for W in the checkpoint's [N, K] layout:
+//  * v_mfma_f32_32x32x16_{f16,bf16}.  The operands are swapped relative to
+//    C = A.W^T: the MFMA's A operand is a 32-row slice of W (32 output columns
+//    n), its B operand a 32-row slice of A (32 tokens m), so each lane's
+//    accumulators hold ONE token and runs of 4 consecutive columns: the
+//    epilogue stores 8-byte packs and finds a gate column and its up column
+//    in the same lane.
+//  * Both operands are K-contiguous in HBM, the natural MFMA operand layout:
+//    no transposition anywhere.  Tiles stream HBM -> LDS with
+//    buffer_load_dwordx4 ... lds (direct to LDS, no VGPR staging) into an
+//    S-stage ring; a stage is waited for with an explicit vmcnt that leaves
+//    the next S-2 stages in flight, so HBM/L2 latency hides behind S-1 stages
+//    of MFMA work.  One s_barrier per stage, without a memory fence (a
+//    workgroup fence would drain every in-flight stage).
+//  * LDS tile rows are 128 bytes (BK = 64 elements, 8 chunks of 16 B); chunk
+//    c of row r sits at c ^ ((r >> 1) & 7), so a fragment read (32 rows x one chunk)
+//    spreads over all banks.  A DMA instruction fills 8 rows (1 KB, one 16 B
+//    chunk per lane): lane l writes physical chunk l & 7 of row l >> 3 and so
+//    fetches that row's logical chunk (l & 7) ^ swz(row).
+//  * Out-of-range rows (m >= M, n >= N) and k chunks (>= this split's end)
+//    get an offset past the buffer's num_records, which the buffer unit
+//    answers with zeros: ragged edges cost nothing and need no padding.
+//  * XCD-aware block order: the hardware deals workgroups round-robin over
+//    the 8 XCDs; units are renumbered so each XCD gets a contiguous range of
+//    tiles (whole n-blocks of W), keeping each weight slice in one L2.
+//  * Split-K: each split writes f32 partials; splitk_reduce_kernel sums them
+//    in split order (deterministic) and runs the epilogue.
+//
+// Epilogues (one 16-bit rounding per output, src/shaders.rs:2045-2073): bias
+// per column (or per row, the channel-major conv), residual add (beta = 1),
+// erf GELU (src/audio_encoder.rs:196-202 on the value of
+// src/shaders.rs:2586-2652) and SiLU.up (src/cpu_decoder.rs:496-505 on the
+// [gate | up] pair src/shaders.rs:1411-1450 reads).
+//
+// gemm_reg_kernel is the W-as-[K, N] form (the reference's `transb` conv
+// operand, src/shaders.rs:1936-1944): register-staged loads that transpose the
+// operand into the same K-contiguous LDS layout.
+#include "qa_internal.h"
+
+namespace qa {
+namespace {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+#define QA_LDS __attribute__((address_space(3)))
+
+constexpr int BK = 64;   // k elements per LDS stage: 128-byte tile rows
+constexpr int NT = 256;  // threads per block (4 waves)
+constexpr uint32_t OOB = 0x80000000u;  // byte offset past every operand's num_records
+
+template <int DT>
+struct Fmt;
+
+template <>
+struct Fmt<QA_F16> {
+  __device__ static __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  __device__ static __forceinline__ float widen(uint32_t h) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+  }
+  // IEEE round-to-nearest-even (v_cvt_f16_f32 in the default round mode).
+  __device__ static __forceinline__ uint32_t narrow(float v) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v);
+  }
+};
+
+template <>
+struct Fmt<QA_BF16> {
+  __device__ static __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  __device__ static __forceinline__ float widen(uint32_t h) { return __uint_as_float(h << 16); }
+  // The storage format's rounding rule, src/shaders.rs:169-179.
+  __device__ static __forceinline__ uint32_t narrow(float v) {
+    const uint32_t u = __float_as_uint(v);
+    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  }
+};
+
+// 16-byte chunk swizzle of an LDS tile row.  gfx950's LDS serves a 16-lane
+// quarter of a ds_read_b128 from 64 banks: rows r and r+1 sit in opposite bank
+// halves (128-byte rows), so pairs of rows share a swizzle value and 16
+// consecutive rows read one logical chunk without a conflict.
+__device__ __forceinline__ int swz(int row) { return (row >> 1) & 7; }
+
+__device__ __forceinline__ int xcd_remap(int b, int n) {
+  constexpr int X = 8;  // XCDs per MI355X
+  const int full = n - n % X;
+  if (b >= full) return b;
+  const int per = full / X;
+  return (b % X) * per + b / X;
+}
+
+// s_waitcnt vmcnt(N) leaving expcnt / lgkmcnt unconstrained (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// Workgroup execution barrier with no memory fence; the asm statements keep
+// the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void exec_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+__device__ __forceinline__ float gelu_erf(float x) {
+  return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f));
+}
+
+__device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
+
+template <int DT>
+__device__ __forceinline__ void store4(uint16_t* p, const float* v) {
+  u32x2 w;
+  w.x = Fmt<DT>::narrow(v[0]) | (Fmt<DT>::narrow(v[1]) << 16);
+  w.y = Fmt<DT>::narrow(v[2]) | (Fmt<DT>::narrow(v[3]) << 16);
+  *reinterpret_cast<u32x2*>(p) = w;
+}
+
+template <int DT>
+__device__ __forceinline__ void widen4(u32x2 w, float* v) {
+  v[0] = Fmt<DT>::widen(w.x & 0xffffu);
+  v[1] = Fmt<DT>::widen(w.x >> 16);
+  v[2] = Fmt<DT>::widen(w.y & 0xffffu);
+  v[3] = Fmt<DT>::widen(w.y >> 16);
+}
+
+// Final values of 4 consecutive output columns [n, n+4) of row m -> C.
+// For SiLU, v holds the gate sums and u the up sums.
+template <int DT, int EPI>
+__device__ __forceinline__ void epilogue4(const GemmParams& p, uint16_t* C, int m, int n,
+                                          const float* v_in, const float* u_in) {
+  uint16_t* dst = C + (int64_t)m * p.ldc + n;
+  float v[4];
+  if constexpr (EPI == EPI_SILU) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float g = Fmt<DT>::widen(Fmt<DT>::narrow(v_in[e]));
+      const float u = Fmt<DT>::widen(Fmt<DT>::narrow(u_in[e]));
+      v[e] = silu_mul(g, u);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = v_in[e];
+    if (p.bias) {
+      if (p.bias_rows) {
+        const float b = Fmt<DT>::widen(p.bias[m]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] += b;
+      } else {
+        float b[4];
+        widen4<DT>(*reinterpret_cast<const u32x2*>(p.bias + n), b);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] += b[e];
+      }
+    }
+    if constexpr (EPI == EPI_GELU) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = gelu_erf(v[e]);
+    }
+    if (p.accumulate) {
+      float old[4];
+      widen4<DT>(*reinterpret_cast<const u32x2*>(dst), old);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] += old[e];
+    }
+  }
+  store4<DT>(dst, v);
+}
+
+// W row for tile row r of n-block tn (SiLU: first half of the tile = gate
+// rows, second half = up rows), or -1 past the edge.
+template <int BN, int EPI>
+__device__ __forceinline__ int w_row(const GemmParams& p, int tn, int r) {
+  if constexpr (EPI == EPI_SILU) {
+    const int half = p.N >> 1, n0h = tn * (BN / 2);
+    const int j = n0h + (r < BN / 2 ? r : r - BN / 2);
+    if (j >= half) return -1;
+    return r < BN / 2 ? j : half + j;
+  } else {
+    const int n = tn * BN + r;
+    return n < p.N ? n : -1;
+  }
+}
+
+// Wave-local 32-column subtile fn -> subtile index within the W tile.
+template <int BN, int FN, int EPI>
+__device__ __forceinline__ int n_subtile(int wn, int fn) {
+  if constexpr (EPI == EPI_SILU) {
+    constexpr int H = FN / 2;
+    return (fn / H) * (BN / 64) + wn * H + (fn % H);
+  } else {
+    return wn * FN + fn;
+  }
+}
+
+// Shared tail: epilogue (splits == 1) or f32 partials (splits > 1).
+// Lane (fr, fh) of MFMA tile (fm, fn) holds token m = .. + fr and columns
+// 8g + 4fh + {0,1,2,3} of the tile's 32-column subtile fn.
+template <int DT, int BM, int BN, int EPI, int FM, int FN, int WTM>
+__device__ __forceinline__ void finish_tile(const GemmParams& p, f32x16 (&acc)[FM][FN], uint16_t* C,
+                                            int tm, int tn, int split, int wm, int wn, int fr,
+                                            int fh) {
+  const int m0 = tm * BM;
+  if (p.splits > 1) {
+    f32x4* ws = reinterpret_cast<f32x4*>(p.ws);
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) {
+      const int m = m0 + wm * WTM + fm * 32 + fr;
+      if (m >= p.M) continue;
+      const int64_t rowbase = ((int64_t)split * p.M + m) * p.N;
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int r = n_subtile<BN, FN, EPI>(wn, fn) * 32 + 8 * g + 4 * fh;
+          const int n = w_row<BN, EPI>(p, tn, r);
+          if (n < 0) continue;
+          const f32x4 v = {acc[fm][fn][4 * g], acc[fm][fn][4 * g + 1], acc[fm][fn][4 * g + 2],
+                           acc[fm][fn][4 * g + 3]};
+          ws[(rowbase + n) >> 2] = v;
+        }
+      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int fm = 0; fm < FM; ++fm) {
+    const int m = m0 + wm * WTM + fm * 32 + fr;
+    if (m >= p.M) continue;
+    if constexpr (EPI == EPI_SILU) {
+      constexpr int H = FN / 2;
+      const int nout = p.N >> 1;
+#pragma unroll
+      for (int fn = 0; fn < H; ++fn) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int n = tn * (BN / 2) + n_subtile<BN, FN, EPI>(wn, fn) * 32 + 8 * g + 4 * fh;
+          if (n >= nout) continue;
+          const float v[4] = {acc[fm][fn][4 * g], acc[fm][fn][4 * g + 1], acc[fm][fn][4 * g + 2],
+                              acc[fm][fn][4 * g + 3]};
+          const float u[4] = {acc[fm][fn + H][4 * g], acc[fm][fn + H][4 * g + 1],
+                              acc[fm][fn + H][4 * g + 2], acc[fm][fn + H][4 * g + 3]};
+          epilogue4<DT, EPI>(p, C, m, n, v, u);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int n = tn * BN + n_subtile<BN, FN, EPI>(wn, fn) * 32 + 8 * g + 4 * fh;
+          if (n >= p.N) continue;
+          const float v[4] = {acc[fm][fn][4 * g], acc[fm][fn][4 * g + 1], acc[fm][fn][4 * g + 2],
+                              acc[fm][fn][4 * g + 3]};
+          epilogue4<DT, EPI>(p, C, m, n, v, nullptr);
+        }
+      }
+    }
+  }
+}
+
+// KG k-groups of 4 waves (256*KG threads).  Every wave issues DMA; group g
+// multiplies slices {g*4/KG .. (g+1)*4/KG - 1} of each 64-deep stage on a
+// 2x2 wave layout, so the LDS read traffic per stage does not grow with KG,
+// while the number of waves streaming L2 -> LDS does (a wave sustains only
+// ~7 B/clk of DMA, so 8 waves per CU are needed to feed the matrix cores).
+// The groups' partial accumulators are summed through LDS at the end, group
+// 0 + group 1 + ..., a fixed order.
+template <int DT, int BM, int BN, int S, int EPI, int KG>
+__global__ void __launch_bounds__(NT * KG) gemm_dma_kernel(const GemmParams p) {
+  constexpr int NTH = NT * KG;
+  constexpr int NW = 4 * KG;       // waves
+  constexpr int SPG = 4 / KG;      // 16-deep slices per group per stage
+  constexpr int WGM = 2, WGN = 2;  // waves along m and n within a group
+  constexpr int WTM = BM / WGM, WTN = BN / WGN;
+  constexpr int FM = WTM / 32, FN = WTN / 32;
+  constexpr int AJ = BM / (8 * NW), BJ = BN / (8 * NW);  // DMA instructions per wave per stage
+  constexpr int LPS = AJ + BJ;
+  constexpr int SA = BM * 128, STAGE = (BM + BN) * 128;
+  constexpr int SMEM = S * STAGE;
+  static_assert(KG == 1 || KG == 2 || KG == 4, "k groups");
+  static_assert(FM >= 1 && FN >= 1 && AJ >= 1 && BJ >= 1, "tile shape");
+  static_assert(BM % (8 * NW) == 0 && BN % (8 * NW) == 0, "DMA row groups");
+  static_assert(EPI != EPI_SILU || FN % 2 == 0, "SiLU pairs gate/up subtiles per wave");
+  static_assert(S >= 2 && (S - 1) * LPS < 64, "pipeline depth");
+  static_assert(KG == 1 || (KG - 1) * 4 * BM * BN <= SMEM, "reduction buffer");
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[SMEM];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int kg = wave >> 2, w4 = wave & 3;
+  const int wm = w4 % WGM, wn = w4 / WGM;
+  const int fr = lane & 31, fh = lane >> 5;  // fragment row, k-chunk parity
+
+  const int units = p.tiles_m * p.tiles_n * p.splits;
+  const int u = xcd_remap((int)blockIdx.x, units);
+  const int split = u % p.splits;
+  const int t = u / p.splits;
+  const int tn = t / p.tiles_m, tm = t % p.tiles_m;
+  const int64_t z = blockIdx.y;
+  const uint16_t* A = p.a + z * p.bsa;
+  const uint16_t* W = p.w + z * p.bsb;
+  uint16_t* C = p.c + z * p.bsc;
+  const __amdgpu_buffer_rsrc_t rsa =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(A), (short)0, p.a_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rsw =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(W), (short)0, p.w_bytes, 0x00020000);
+
+  const int m0 = tm * BM;
+  const int kbeg = split * p.kchunk;
+  const int kend = min(p.K, kbeg + p.kchunk);
+  const int nk = (kend - kbeg + BK - 1) / BK;
+
+  // Per-lane byte offsets at k = 0 of the row chunk this lane fetches: lane l
+  // of DMA instruction j fills LDS row r = (NW*j + wave)*8 + l/8 at physical
+  // chunk l%8, so it fetches logical chunk (l%8) ^ swz(r).
+  const int lrow = lane >> 3, pchunk = lane & 7;
+  uint32_t aoff[AJ], woff[BJ];
+  int akc[AJ], wkc[BJ];  // k offset (elements) of the fetched chunk
+#pragma unroll
+  for (int j = 0; j < AJ; ++j) {
+    const int r = (j * NW + wave) * 8 + lrow;
+    const int m = m0 + r;
+    akc[j] = (pchunk ^ swz(r)) * 8;
+    aoff[j] = m < p.M ? (uint32_t)(((int64_t)m * p.lda + akc[j]) * 2) : OOB;
+  }
+#pragma unroll
+  for (int j = 0; j < BJ; ++j) {
+    const int r = (j * NW + wave) * 8 + lrow;
+    const int n = w_row<BN, EPI>(p, tn, r);
+    wkc[j] = (pchunk ^ swz(r)) * 8;
+    woff[j] = n >= 0 ? (uint32_t)(((int64_t)n * p.ldb + wkc[j]) * 2) : OOB;
+  }
+
+  auto issue = [&](int kidx, int buf) {
+    const int k0 = kbeg + kidx * BK;
+    unsigned char* sb = smem + buf * STAGE;
+#pragma unroll
+    for (int j = 0; j < AJ; ++j) {
+      const bool ok = k0 + akc[j] < kend && aoff[j] != OOB;
+      const uint32_t off = ok ? aoff[j] + (uint32_t)k0 * 2u : OOB;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (QA_LDS void*)(sb + (j * NW + wave) * 1024),
+                                               16, off, 0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < BJ; ++j) {
+      const bool ok = k0 + wkc[j] < kend && woff[j] != OOB;
+      const uint32_t off = ok ? woff[j] + (uint32_t)k0 * 2u : OOB;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rsw, (QA_LDS void*)(sb + SA + (j * NW + wave) * 1024), 16, off, 0, 0, 0);
+    }
+  };
+
+  f32x16 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = f32x16{0};
+
+  // Fragments of one 16-deep k slice, double-buffered in registers.
+  u32x4 fa[2][FN], fb[2][FM];
+  auto read_frags = [&](int buf, int kk, int slot) {
+    const unsigned char* sA = smem + buf * STAGE;
+    const unsigned char* sB = sA + SA;
+    const int c = kk * 2 + fh;
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn) {
+      const int row = n_subtile<BN, FN, EPI>(wn, fn) * 32 + fr;
+      fa[slot][fn] = *reinterpret_cast<const u32x4*>(sB + row * 128 + ((c ^ swz(row)) << 4));
+    }
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) {
+      const int row = wm * WTM + fm * 32 + fr;
+      fb[slot][fm] = *reinterpret_cast<const u32x4*>(sA + row * 128 + ((c ^ swz(row)) << 4));
+    }
+  };
+  auto mma = [&](int slot) {
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn)
+        acc[fm][fn] = Fmt<DT>::mfma(fa[slot][fn], fb[slot][fm], acc[fm][fn]);
+  };
+
+  // Pipeline: all S buffers are filled up front; the fragments of the next
+  // slice are read while the current one multiplies; the barrier that
+  // publishes stage it+1 (and frees stage it's buffer for stage it+S) comes
+  // after the stage's last MFMAs are issued, so it overlaps matrix-core work.
+  const int kk0 = kg * SPG;
+  if (nk > 0) {
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+      if (s < nk) issue(s, s);
+    if (S - 1 < nk)
+      wait_vmcnt<(S - 1) * LPS>();
+    else
+      wait_vmcnt<0>();
+    exec_barrier();
+    read_frags(0, kk0, 0);
+    for (int it = 0; it < nk; ++it) {
+      const int buf = it % S;
+#pragma unroll
+      for (int q = 0; q < SPG; ++q) {
+        if (q + 1 < SPG) read_frags(buf, kk0 + q + 1, (q + 1) & 1);
+        mma(q & 1);
+      }
+      if (it + 1 < nk) {
+        if (it + S - 1 < nk)
+          wait_vmcnt<(S - 2) * LPS>();
+        else
+          wait_vmcnt<0>();
+        exec_barrier();
+        if (it + S < nk) issue(it + S, buf);
+        read_frags((it + 1) % S, kk0, 0);
+      }
+    }
+  }
+
+  if constexpr (KG > 1) {
+    // Sum the k-groups' partials: groups 1.. park theirs in LDS (lane-major,
+    // conflict-free), group 0 adds them in group order.
+    constexpr int R = FM * FN * 16;  // accumulator registers per lane
+    float* red = reinterpret_cast<float*>(smem);
+    __syncthreads();  // every wave is past its last LDS read of the stages
+    if (kg > 0) {
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            red[(((kg - 1) * 4 + w4) * R + (fm * FN + fn) * 16 + r) * 64 + lane] = acc[fm][fn][r];
+    }
+    __syncthreads();
+    if (kg > 0) return;
+#pragma unroll
+    for (int g = 1; g < KG; ++g)
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            acc[fm][fn][r] += red[(((g - 1) * 4 + w4) * R + (fm * FN + fn) * 16 + r) * 64 + lane];
+  }
+  finish_tile<DT, BM, BN, EPI, FM, FN, WTM>(p, acc, C, tm, tn, split, wm, wn, fr, fh);
+}
+
+// W as [K, N] (row stride ldb): register-staged, double-buffered; each
+// 16-byte load (8 consecutive n of one k row) is scattered into the
+// K-contiguous LDS layout the MFMA fragments read.
+template <int DT, int EPI>
+__global__ void __launch_bounds__(NT) gemm_reg_kernel(const GemmParams p) {
+  constexpr int BM = 128, BN = 128;
+  constexpr int WGM = 2;
+  constexpr int WTM = 64;
+  constexpr int FM = 2, FN = 2;
+  constexpr int AP = BM * 8 / NT, BP = BN * 8 / NT;
+  constexpr int SA = BM * 128, SB = BN * 128;
+  __shared__ __attribute__((aligned(16))) unsigned char smem[2 * (SA + SB)];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave % WGM, wn = wave / WGM;
+  const int fr = lane & 31, fh = lane >> 5;
+
+  const int units = p.tiles_m * p.tiles_n * p.splits;
+  const int u = xcd_remap((int)blockIdx.x, units);
+  const int split = u % p.splits;
+  const int t = u / p.splits;
+  const int tn = t / p.tiles_m, tm = t % p.tiles_m;
+  const int64_t z = blockIdx.y;
+  const uint16_t* __restrict__ A = p.a + z * p.bsa;
+  const uint16_t* __restrict__ W = p.w + z * p.bsb;
+  uint16_t* C = p.c + z * p.bsc;
+
+  const int m0 = tm * BM;
+  const int kbeg = split * p.kchunk;
+  const int kend = min(p.K, kbeg + p.kchunk);
+  const int nk = (kend - kbeg + BK - 1) / BK;
+
+  const int ch = tid & 7, rsub = tid >> 3;
+  const uint16_t* aptr[AP];
+  bool arow_ok[AP];
+#pragma unroll
+  for (int i = 0; i < AP; ++i) {
+    const int r = m0 + i * 32 + rsub;
+    arow_ok[i] = r < p.M;
+    aptr[i] = A + (int64_t)min(r, p.M - 1) * p.lda + ch * 8;
+  }
+
+  u32x4 ra[AP], rb[BP];
+  auto load_stage = [&](int k0) {
+    const bool kin = k0 + ch * 8 < kend;
+#pragma unroll
+    for (int i = 0; i < AP; ++i)
+      ra[i] = (kin && arow_ok[i]) ? *reinterpret_cast<const u32x4*>(aptr[i] + k0)
+                                  : u32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < BP; ++i) {
+      const int q = i * NT + tid;
+      const int krow = q / (BN / 8), nc = q % (BN / 8);
+      const int gk = k0 + krow, gn = tn * BN + nc * 8;
+      rb[i] = (gk < kend && gn < p.N)
+                  ? *reinterpret_cast<const u32x4*>(W + (int64_t)gk * p.ldb + gn)
+                  : u32x4{0, 0, 0, 0};
+    }
+  };
+  auto store_stage = [&](int stage) {
+    unsigned char* sA = smem + stage * (SA + SB);
+    unsigned char* sB = sA + SA;
+#pragma unroll
+    for (int i = 0; i < AP; ++i) {
+      const int row = i * 32 + rsub;
+      *reinterpret_cast<u32x4*>(sA + row * 128 + ((ch ^ swz(row)) << 4)) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < BP; ++i) {
+      const int q = i * NT + tid;
+      const int krow = q / (BN / 8), nc = q % (BN / 8);
+      const uint32_t w4[4] = {rb[i].x, rb[i].y, rb[i].z, rb[i].w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int row = nc * 8 + e;
+        const uint16_t v = (uint16_t)(w4[e >> 1] >> ((e & 1) * 16));
+        *reinterpret_cast<uint16_t*>(sB + row * 128 + (((krow >> 3) ^ swz(row)) << 4) +
+                                     (krow & 7) * 2) = v;
+      }
+    }
+  };
+
+  f32x16 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = f32x16{0};
+
+  auto compute_stage = [&](int stage) {
+    const unsigned char* sA = smem + stage * (SA + SB);
+    const unsigned char* sB = sA + SA;
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; ++kk) {
+      const int c = kk * 2 + fh;
+      u32x4 fa[FN], fb[FM];
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn) {
+        const int row = (wn * FN + fn) * 32 + fr;
+        fa[fn] = *reinterpret_cast<const u32x4*>(sB + row * 128 + ((c ^ swz(row)) << 4));
+      }
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm) {
+        const int row = wm * WTM + fm * 32 + fr;
+        fb[fm] = *reinterpret_cast<const u32x4*>(sA + row * 128 + ((c ^ swz(row)) << 4));
+      }
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn) acc[fm][fn] = Fmt<DT>::mfma(fa[fn], fb[fm], acc[fm][fn]);
+    }
+  };
+
+  if (nk > 0) {
+    load_stage(kbeg);
+    store_stage(0);
+    __syncthreads();
+    for (int it = 0; it < nk; ++it) {
+      const bool more = it + 1 < nk;
+      if (more) load_stage(kbeg + (it + 1) * BK);
+      compute_stage(it & 1);
+      if (more) store_stage((it + 1) & 1);
+      __syncthreads();
+    }
+  }
+  finish_tile<DT, BM, BN, EPI, FM, FN, WTM>(p, acc, C, tm, tn, split, wm, wn, fr, fh);
+}
+
+// Sum the split-K partials [splits][M][N] (f32) in split order and run the
+// epilogue: one thread per 4 output columns of one row.
+template <int DT, int EPI>
+__global__ void __launch_bounds__(256) splitk_reduce_kernel(const GemmParams p) {
+  const int nout = EPI == EPI_SILU ? p.N / 2 : p.N;
+  const int groups = nout / 4;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)p.M * groups) return;
+  const int m = (int)(idx / groups), n = (int)(idx % groups) * 4;
+  const f32x4* ws = reinterpret_cast<const f32x4*>(p.ws);
+  f32x4 s = {0.f, 0.f, 0.f, 0.f}, su = {0.f, 0.f, 0.f, 0.f};
+  for (int sp = 0; sp < p.splits; ++sp) {
+    const int64_t row = ((int64_t)sp * p.M + m) * p.N;
+    s += ws[(row + n) >> 2];
+    if constexpr (EPI == EPI_SILU) su += ws[(row + nout + n) >> 2];
+  }
+  const float v[4] = {s.x, s.y, s.z, s.w};
+  const float uu[4] = {su.x, su.y, su.z, su.w};
+  epilogue4<DT, EPI>(p, p.c, m, n, v, uu);
+}
+
+template <int DT, int BM, int BN, int S, int EPI, int KG>
+hipError_t launch_dma(const Plan& plan, const GemmParams& p, int batch, hipStream_t s) {
+  const unsigned units = (unsigned)(plan.tiles_m * plan.tiles_n * plan.splits);
+  hipLaunchKernelGGL((gemm_dma_kernel<DT, BM, BN, S, EPI, KG>), dim3(units, (unsigned)batch),
+                     dim3(NT * KG), 0, s, p);
+  return hipGetLastError();
+}
+
+template <int DT, int EPI>
+hipError_t launch_reg(const Plan& plan, const GemmParams& p, int batch, hipStream_t s) {
+  const unsigned units = (unsigned)(plan.tiles_m * plan.tiles_n * plan.splits);
+  hipLaunchKernelGGL((gemm_reg_kernel<DT, EPI>), dim3(units, (unsigned)batch), dim3(NT), 0, s, p);
+  return hipGetLastError();
+}
+
+template <int DT, int EPI>
+hipError_t launch_reduce(const GemmParams& p, hipStream_t s) {
+  const int nout = EPI == EPI_SILU ? p.N / 2 : p.N;
+  const int64_t threads = (int64_t)p.M * (nout / 4);
+  hipLaunchKernelGGL((splitk_reduce_kernel<DT, EPI>), dim3((unsigned)((threads + 255) / 256)),
+                     dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
+template <int DT, int EPI>
+hipError_t launch_epi(const Plan& plan, const GemmParams& p, int batch, hipStream_t s) {
+  hipError_t e;
+  if (plan.transb) {
+    if constexpr (EPI == EPI_SILU) return hipErrorInvalidValue;  // rejected by validation
+    else e = launch_reg<DT, EPI>(plan, p, batch, s);
+  } else {
+    switch (plan.tile) {
+      case TILE_256x128: e = launch_dma<DT, 256, 128, 3, EPI, 2>(plan, p, batch, s); break;
+      case TILE_128x256: e = launch_dma<DT, 128, 256, 3, EPI, 2>(plan, p, batch, s); break;
+      case TILE_64x128: e = launch_dma<DT, 64, 128, 4, EPI, 2>(plan, p, batch, s); break;
+      default: e = launch_dma<DT, 128, 128, 4, EPI, 2>(plan, p, batch, s); break;
+    }
+  }
+  if (e != hipSuccess || plan.splits == 1) return e;
+  return launch_reduce<DT, EPI>(p, s);
+}
+
+template <int DT>
+hipError_t launch_dt(const Plan& plan, const GemmParams& p, int batch, hipStream_t s) {
+  switch (plan.epi) {
+    case EPI_GELU: return launch_epi<DT, EPI_GELU>(plan, p, batch, s);
+    case EPI_SILU: return launch_epi<DT, EPI_SILU>(plan, p, batch, s);
+    default: return launch_epi<DT, EPI_PLAIN>(plan, p, batch, s);
+  }
+}
+
+}  // namespace
+
+hipError_t launch_gemm(int dtype, const Plan& plan, const GemmParams& p, int batch,
+                       hipStream_t stream) {
+  if (dtype == QA_BF16) return launch_dt<QA_BF16>(plan, p, batch, stream);
+  return launch_dt<QA_F16>(plan, p, batch, stream);
+}
+
+}  // namespace qa

@@ -1,0 +1,69 @@
+// qa_internal.h -- shared between the C-ABI layer (qa_api.cpp) and the
+// kernels (qa_gemm.hip).  Not installed; the public surface is include/qa.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "qa.h"
+
+namespace qa {
+
+// Epilogue kinds compiled into separate kernels.  Bias and the residual add
+// are runtime switches of EPI_PLAIN (they cost one branch in the epilogue);
+// GELU and SiLU-mul change the epilogue's arithmetic and its column mapping.
+enum Epi : int { EPI_PLAIN = 0, EPI_GELU = 1, EPI_SILU = 2 };
+
+// Tile shapes (block BM x BN, 4 waves).  Chosen per call by plan_linear().
+enum TileCfg : int {
+  TILE_128x128 = 0,  // 2x2 waves of 64x64
+  TILE_256x128 = 1,  // 2x2 waves of 128(m) x 64(n)
+  TILE_128x256 = 2,  // 2x2 waves of 64(m) x 128(n)
+  TILE_64x128 = 3,   // 2x2 waves of 32(m) x 64(n)
+  TILE_COUNT
+};
+
+struct TileShape {
+  int bm, bn;
+};
+inline TileShape tile_shape(int cfg) {
+  switch (cfg) {
+    case TILE_256x128: return {256, 128};
+    case TILE_128x256: return {128, 256};
+    case TILE_64x128: return {64, 128};
+    default: return {128, 128};
+  }
+}
+
+// Kernel parameters (passed by value).  Element units throughout.
+struct GemmParams {
+  const uint16_t* a;
+  const uint16_t* w;
+  uint16_t* c;
+  const uint16_t* bias;  // nullptr = no bias
+  float* ws;             // split-K partials [splits][M][N] f32 (splits > 1)
+  int a_bytes, w_bytes;  // byte span of one batch's A / W (buffer num_records)
+  int M, N, K;           // N = rows of W (2*inter for SiLU-mul)
+  int lda, ldb, ldc;
+  int64_t bsa, bsb, bsc;
+  int tiles_m, tiles_n;  // output tiles
+  int splits;            // K splits per tile (>= 1)
+  int kchunk;            // K range per split, multiple of 64
+  int accumulate;        // add C_old before the rounding
+  int bias_rows;         // bias indexed by output row (channel-major conv)
+};
+
+struct Plan {
+  int tile;
+  int epi;
+  bool transb;
+  int tiles_m, tiles_n, splits, kchunk;
+  size_t ws_floats;   // split-K partial floats needed
+};
+
+// Launch one planned GEMM on `stream` (grid = tiles*splits x batch).
+hipError_t launch_gemm(int dtype, const Plan& plan, const GemmParams& p, int batch,
+                       hipStream_t stream);
+
+
+}  // namespace qa

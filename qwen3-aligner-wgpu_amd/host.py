@@ -1,0 +1,199 @@
+"""ctypes view of csrc/libqa_host.so (csrc/host/qa_host.h): the C++ host
+mirror of the reference's GEMM call sites, plus the synthetic-input generator.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from . import check, host_lib
+
+_vp = ctypes.c_void_p
+_i = ctypes.c_int
+_u64 = ctypes.c_uint64
+_sz = ctypes.c_size_t
+_dp = ctypes.POINTER(ctypes.c_double)
+
+
+def declare(L: ctypes.CDLL) -> None:
+    L.qah_synth_normal_h16.argtypes = [_u64, _u64, ctypes.c_float, ctypes.c_float, _i, _vp, _sz]
+    L.qah_synth_normal_h16.restype = None
+    L.qah_synth_normal_f32.argtypes = [_u64, _u64, ctypes.c_float, ctypes.c_float, _vp, _sz]
+    L.qah_synth_normal_f32.restype = None
+    L.qah_narrow_f32.argtypes = [_vp, _vp, _sz, _i]
+    L.qah_narrow_f32.restype = None
+    L.qah_concat_rows.argtypes = [ctypes.POINTER(_vp), ctypes.POINTER(ctypes.c_int64), _i,
+                                  ctypes.c_int64, _vp]
+    L.qah_concat_rows.restype = None
+    L.qah_decoder_create.argtypes = [_vp, _i, _i, _i, _i, _i, _i, _i, ctypes.POINTER(_vp)]
+    L.qah_decoder_load_layer.argtypes = [_vp, _i] + [_vp] * 7
+    L.qah_decoder_set_inputs.argtypes = [_vp, _i, _vp, _vp, _vp, _vp]
+    L.qah_decoder_prefill_linears.argtypes = [_vp, _i]
+    L.qah_decoder_read.argtypes = [_vp, _i, _i, _vp]
+    L.qah_decoder_time.argtypes = [_vp, _i, _i, _i, _i, _dp]
+    L.qah_decoder_profile_sites.argtypes = [_vp, _i, _i, _dp]
+    L.qah_decoder_destroy.argtypes = [_vp]
+    L.qah_decoder_destroy.restype = None
+    L.qah_encoder_create.argtypes = [_vp, _i, _i, _i, _i, _i, _i, ctypes.POINTER(_vp)]
+    L.qah_encoder_load_layer.argtypes = [_vp, _i] + [_vp] * 8
+    L.qah_encoder_load_conv.argtypes = [_vp, _vp, _vp]
+    L.qah_encoder_set_inputs.argtypes = [_vp, _i, _vp, _vp, _vp, _vp, _vp]
+    L.qah_encoder_forward_linears.argtypes = [_vp, _i]
+    L.qah_encoder_read.argtypes = [_vp, _i, _i, _vp]
+    L.qah_encoder_time.argtypes = [_vp, _i, _i, _i, _i, _dp]
+    L.qah_encoder_profile_sites.argtypes = [_vp, _i, _i, _dp]
+    L.qah_encoder_destroy.argtypes = [_vp]
+    L.qah_encoder_destroy.restype = None
+    L.qah_time_linear.argtypes = [_vp, _vp, _i, _i, _dp]
+    for name in ("qah_decoder_create", "qah_decoder_load_layer", "qah_decoder_set_inputs",
+                 "qah_decoder_prefill_linears", "qah_decoder_read", "qah_decoder_time",
+                 "qah_decoder_profile_sites", "qah_encoder_create", "qah_encoder_load_layer",
+                 "qah_encoder_load_conv", "qah_encoder_set_inputs", "qah_encoder_forward_linears",
+                 "qah_encoder_read", "qah_encoder_time", "qah_encoder_profile_sites",
+                 "qah_time_linear"):
+        getattr(L, name).restype = _i
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data
+
+
+def synth_normal(seed: int, tensor_id: int, shape, mean: float = 0.0, std: float = 1.0,
+                 dtype: int = 0) -> np.ndarray:
+    """Seeded N(mean, std^2) values as 16-bit bits (SplitMix64 + Box-Muller)."""
+    out = np.empty(shape, np.uint16)
+    host_lib().qah_synth_normal_h16(seed, tensor_id, mean, std, dtype, out.ctypes.data, out.size)
+    return out
+
+
+def synth_normal_f32(seed: int, tensor_id: int, shape, mean: float = 0.0,
+                     std: float = 1.0) -> np.ndarray:
+    out = np.empty(shape, np.float32)
+    host_lib().qah_synth_normal_f32(seed, tensor_id, mean, std, out.ctypes.data, out.size)
+    return out
+
+
+def narrow(x: np.ndarray, dtype: int) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty(x.shape, np.uint16)
+    host_lib().qah_narrow_f32(x.ctypes.data, out.ctypes.data, x.size, dtype)
+    return out
+
+
+def concat_rows(parts) -> np.ndarray:
+    parts = [np.ascontiguousarray(p, np.uint16) for p in parts]
+    cols = parts[0].shape[1]
+    assert all(p.shape[1] == cols for p in parts)
+    out = np.empty((sum(p.shape[0] for p in parts), cols), np.uint16)
+    ptrs = (_vp * len(parts))(*[p.ctypes.data for p in parts])
+    rows = (ctypes.c_int64 * len(parts))(*[p.shape[0] for p in parts])
+    host_lib().qah_concat_rows(ptrs, rows, len(parts), cols, out.ctypes.data)
+    return out
+
+
+class DecoderLinears:
+    """qah_decoder: the text decoder's per-layer projections."""
+
+    def __init__(self, ctx, dtype: int, layers: int, max_rows: int, hidden: int = 1024,
+                 q_dim: int = 2048, kv_dim: int = 1024, inter: int = 3072):
+        self.ctx, self.dtype, self.layers, self.max_rows = ctx, dtype, layers, max_rows
+        self.hidden, self.q_dim, self.kv_dim, self.inter = hidden, q_dim, kv_dim, inter
+        h = _vp()
+        check(host_lib().qah_decoder_create(ctx.handle, dtype, layers, hidden, q_dim, kv_dim,
+                                            inter, max_rows, ctypes.byref(h)))
+        self.handle = h.value
+
+    def close(self):
+        if self.handle:
+            host_lib().qah_decoder_destroy(self.handle)
+            self.handle = None
+
+    def load_layer(self, li, q, k, v, o, gate, up, down):
+        arrs = [np.ascontiguousarray(a, np.uint16) for a in (q, k, v, o, gate, up, down)]
+        check(host_lib().qah_decoder_load_layer(self.handle, li, *[_p(a) for a in arrs]))
+
+    def set_inputs(self, rows, normed=None, attn=None, norm2=None, h=None):
+        check(host_lib().qah_decoder_set_inputs(self.handle, rows, _p(normed), _p(attn),
+                                                _p(norm2), _p(h)))
+
+    def prefill_linears(self, rows):
+        check(host_lib().qah_decoder_prefill_linears(self.handle, rows))
+
+    def read(self, which: str, rows: int) -> np.ndarray:
+        idx, cols = {"h": (0, self.hidden), "qkv": (1, self.q_dim + 2 * self.kv_dim),
+                     "act": (2, self.inter)}[which]
+        out = np.empty((rows, cols), np.uint16)
+        check(host_lib().qah_decoder_read(self.handle, idx, rows, out.ctypes.data))
+        return out
+
+    def time(self, rows, warmup, steps, use_graph=True) -> float:
+        ms = ctypes.c_double()
+        check(host_lib().qah_decoder_time(self.handle, rows, warmup, steps, int(use_graph),
+                                          ctypes.byref(ms)))
+        return ms.value
+
+    def profile_sites(self, rows, steps) -> dict:
+        out = (ctypes.c_double * 4)()
+        check(host_lib().qah_decoder_profile_sites(self.handle, rows, steps, out))
+        return dict(zip(("qkv", "o", "gu", "down"), list(out)))
+
+
+class EncoderLinears:
+    """qah_encoder: the audio tower's linears + the conv block GEMM."""
+
+    def __init__(self, ctx, dtype: int, layers: int, max_rows: int, d_model: int = 896,
+                 ffn: int = 3584, conv_k: int = 1152):
+        self.ctx, self.dtype, self.layers, self.max_rows = ctx, dtype, layers, max_rows
+        self.d_model, self.ffn, self.conv_k = d_model, ffn, conv_k
+        h = _vp()
+        check(host_lib().qah_encoder_create(ctx.handle, dtype, layers, d_model, ffn, conv_k,
+                                            max_rows, ctypes.byref(h)))
+        self.handle = h.value
+
+    def close(self):
+        if self.handle:
+            host_lib().qah_encoder_destroy(self.handle)
+            self.handle = None
+
+    def load_layer(self, li, qkv_w, qkv_b, o_w, o_b, fc1_w, fc1_b, fc2_w, fc2_b):
+        arrs = [np.ascontiguousarray(a, np.uint16)
+                for a in (qkv_w, qkv_b, o_w, o_b, fc1_w, fc1_b, fc2_w, fc2_b)]
+        check(host_lib().qah_encoder_load_layer(self.handle, li, *[_p(a) for a in arrs]))
+
+    def load_conv(self, w, b):
+        w = np.ascontiguousarray(w, np.uint16)
+        b = np.ascontiguousarray(b, np.uint16)
+        check(host_lib().qah_encoder_load_conv(self.handle, _p(w), _p(b)))
+
+    def set_inputs(self, rows, col=None, normed=None, attn=None, norm2=None, h=None):
+        check(host_lib().qah_encoder_set_inputs(self.handle, rows, _p(col), _p(normed),
+                                                _p(attn), _p(norm2), _p(h)))
+
+    def forward_linears(self, rows):
+        check(host_lib().qah_encoder_forward_linears(self.handle, rows))
+
+    def read(self, which: str, rows: int) -> np.ndarray:
+        idx, cols = {"h": (0, self.d_model), "conv": (1, self.d_model),
+                     "qkv": (2, 3 * self.d_model), "act": (3, self.ffn)}[which]
+        out = np.empty((rows, cols), np.uint16)
+        check(host_lib().qah_encoder_read(self.handle, idx, rows, out.ctypes.data))
+        return out
+
+    def time(self, rows, warmup, steps, use_graph=True) -> float:
+        ms = ctypes.c_double()
+        check(host_lib().qah_encoder_time(self.handle, rows, warmup, steps, int(use_graph),
+                                          ctypes.byref(ms)))
+        return ms.value
+
+    def profile_sites(self, rows, steps) -> dict:
+        out = (ctypes.c_double * 5)()
+        check(host_lib().qah_encoder_profile_sites(self.handle, rows, steps, out))
+        return dict(zip(("conv", "qkv", "o", "fc1", "fc2"), list(out)))
+
+
+def time_linear(ctx, desc, warmup: int, iters: int) -> float:
+    ms = ctypes.c_double()
+    check(host_lib().qah_time_linear(ctx.handle, ctypes.byref(desc), warmup, iters,
+                                     ctypes.byref(ms)))
+    return ms.value
