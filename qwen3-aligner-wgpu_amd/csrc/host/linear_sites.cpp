@@ -11,6 +11,7 @@
 #include "linear_sites.hpp"
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstring>
 #include <thread>
@@ -380,7 +381,8 @@ namespace {
 
 // Runs `step` warmup + steps times; optional graph capture of one step.
 template <class Step>
-int time_steps(qa_ctx* ctx, int warmup, int steps, int use_graph, Step&& step, double* ms) {
+int time_steps(qa_ctx* ctx, int warmup, int steps, int use_graph, Step&& step, double* ms,
+               double* wall_ms = nullptr) {
   hipStream_t s = (hipStream_t)qa_ctx_stream(ctx);
   for (int i = 0; i < warmup; ++i)
     if (int rc = step()) return rc;
@@ -400,6 +402,7 @@ int time_steps(qa_ctx* ctx, int warmup, int steps, int use_graph, Step&& step, d
   hipEvent_t e0, e1;
   (void)hipEventCreate(&e0);
   (void)hipEventCreate(&e1);
+  const auto w0 = std::chrono::steady_clock::now();
   (void)hipEventRecord(e0, s);
   int rc = QA_OK;
   for (int i = 0; i < steps && rc == QA_OK; ++i) {
@@ -410,6 +413,9 @@ int time_steps(qa_ctx* ctx, int warmup, int steps, int use_graph, Step&& step, d
   }
   (void)hipEventRecord(e1, s);
   const int rs = qa_sync(ctx);
+  const auto w1 = std::chrono::steady_clock::now();
+  if (wall_ms && steps > 0)
+    *wall_ms = std::chrono::duration<double, std::milli>(w1 - w0).count() / steps;
   float t = 0.f;
   (void)hipEventElapsedTime(&t, e0, e1);
   (void)hipEventDestroy(e0);
@@ -491,10 +497,10 @@ int qah_decoder_read(qah_decoder* d, int which, int rows, uint16_t* host) {
 }
 
 int qah_decoder_time(qah_decoder* d, int rows, int warmup, int steps, int use_graph,
-                     double* ms_per_step) {
+                     double* ms_per_step, double* wall_ms_per_step) {
   if (!d || !ms_per_step) return QA_EINVAL;
   return time_steps(d->d->ctx, warmup, steps, use_graph,
-                    [&] { return d->d->prefill_linears(rows); }, ms_per_step);
+                    [&] { return d->d->prefill_linears(rows); }, ms_per_step, wall_ms_per_step);
 }
 
 int qah_decoder_profile_sites(qah_decoder* d, int rows, int steps, double* site_ms) {
@@ -562,10 +568,10 @@ int qah_encoder_read(qah_encoder* e, int which, int rows, uint16_t* host) {
 }
 
 int qah_encoder_time(qah_encoder* e, int rows, int warmup, int steps, int use_graph,
-                     double* ms_per_step) {
+                     double* ms_per_step, double* wall_ms_per_step) {
   if (!e || !ms_per_step) return QA_EINVAL;
   return time_steps(e->e->ctx, warmup, steps, use_graph,
-                    [&] { return e->e->forward_linears(rows); }, ms_per_step);
+                    [&] { return e->e->forward_linears(rows); }, ms_per_step, wall_ms_per_step);
 }
 
 int qah_encoder_profile_sites(qah_encoder* e, int rows, int steps, double* site_ms) {

@@ -67,10 +67,12 @@ int qah_decoder_prefill_linears(qah_decoder* d, int rows);
 /* Copy back: which = 0 h [rows, hidden], 1 qkv [rows, q+2kv] of the last
  * layer run, 2 act [rows, inter] of the last layer run. */
 int qah_decoder_read(qah_decoder* d, int which, int rows, uint16_t* host);
-/* Time `steps` forward passes after `warmup` (HIP events on the context's
- * stream).  use_graph = 1 replays one captured hipGraph per step. */
+/* Time `steps` forward passes after `warmup`: HIP events on the context's
+ * stream (ms_per_step) and the host clock from the first launch to the
+ * completed synchronize (wall_ms_per_step, may be NULL).  use_graph = 1
+ * replays one captured hipGraph per step. */
 int qah_decoder_time(qah_decoder* d, int rows, int warmup, int steps, int use_graph,
-                     double* ms_per_step);
+                     double* ms_per_step, double* wall_ms_per_step);
 /* Per-site average kernel duration (ms) over `steps` passes, each launch
  * bracketed by its own pair of HIP events: site_ms[0..3] = qkv, o, gu, down. */
 int qah_decoder_profile_sites(qah_decoder* d, int rows, int steps, double* site_ms);
@@ -100,7 +102,7 @@ int qah_encoder_forward_linears(qah_encoder* e, int rows);
  * 3 act [rows, ffn] of the last layer run. */
 int qah_encoder_read(qah_encoder* e, int which, int rows, uint16_t* host);
 int qah_encoder_time(qah_encoder* e, int rows, int warmup, int steps, int use_graph,
-                     double* ms_per_step);
+                     double* ms_per_step, double* wall_ms_per_step);
 /* site_ms[0..4] = conv, qkv, o, fc1, fc2 */
 int qah_encoder_profile_sites(qah_encoder* e, int rows, int steps, double* site_ms);
 void qah_encoder_destroy(qah_encoder* e);

@@ -128,10 +128,26 @@ int validate(const qa_linear_desc* d) {
   return ok();
 }
 
-// Tile / split-K choice.  Units (tiles x splits) should cover the CUs at
-// least once; among tile shapes, prefer the one with the fewest "rounds" of
-// work per CU, measured in 128x128x64 MFMA-stage equivalents, then the
-// larger tile (fewer operand bytes per flop).
+// Measured on MI355X (gfx950) with the kernels of qa_gemm.hip: time per
+// 64-deep k stage of one tile with one block per CU (the L2 -> LDS stream
+// sets it, not the matrix cores), and the fixed cost of a tile (block start
+// skew + prologue fill + epilogue), in microseconds.
+double stage_us(int tile) {
+  switch (tile) {
+    case qa::TILE_256x128:
+    case qa::TILE_128x256: return 1.10;
+    case qa::TILE_64x128: return 0.34;
+    case qa::TILE_64x64: return 0.26;
+    default: return 0.60;
+  }
+}
+constexpr double kTileFixedUs = 3.0;
+constexpr double kLaunchUs = 2.0;       // one more kernel in the stream (split-K reduce)
+constexpr double kReduceGBs = 3000.0;   // split-K reduce kernel, partials from L2/MALL
+
+// Tile / split-K choice: the modelled time of each candidate is
+// rounds x (fixed + stages x stage_us) (+ the reduce kernel when K is split),
+// where rounds = ceil(units / CUs); the cheapest candidate wins.
 qa::Plan plan_linear(const qa_linear_desc& d, int num_cus) {
   qa::Plan pl{};
   const bool silu = d.flags & QA_EPI_SILU_MUL;
@@ -145,10 +161,11 @@ qa::Plan plan_linear(const qa_linear_desc& d, int num_cus) {
   if (const char* e = getenv("QA_SPLITS")) forced_splits = atoi(e);
 
   int cands[qa::TILE_COUNT] = {qa::TILE_128x128, qa::TILE_256x128, qa::TILE_128x256,
-                               qa::TILE_64x128};
-  int ncand = qa::TILE_COUNT;
+                               qa::TILE_64x128, qa::TILE_64x64};
+  int ncand = silu ? qa::TILE_COUNT - 1 : qa::TILE_COUNT;  // 64x64 cannot pair gate/up
   if (pl.transb) ncand = 1;  // the conv operand path has one tile shape
-  if (forced_tile >= 0 && forced_tile < qa::TILE_COUNT && !pl.transb) {
+  if (forced_tile >= 0 && forced_tile < qa::TILE_COUNT && !pl.transb &&
+      !(silu && forced_tile == qa::TILE_64x64)) {
     cands[0] = forced_tile;
     ncand = 1;
   }
@@ -158,31 +175,25 @@ qa::Plan plan_linear(const qa_linear_desc& d, int num_cus) {
     const int64_t tbn = silu ? ts.bn / 2 : ts.bn;
     const int64_t tm = (M + ts.bm - 1) / ts.bm, tn = (nout + tbn - 1) / tbn;
     const int64_t tiles = tm * tn;
-    int64_t splits = 1;
-    if (forced_splits > 0) {
-      splits = forced_splits;
-    } else {
-      // Split K while the units leave at least a quarter of the CUs idle and
-      // each split keeps >= 256 of k (4 LDS stages).
-      while (tiles * splits * 4 < (int64_t)num_cus * 3 && K / (splits * 2) >= 256) splits *= 2;
-    }
-    int64_t kchunk = ((K + splits - 1) / splits + 63) / 64 * 64;
-    splits = (K + kchunk - 1) / kchunk;
-    const int64_t units = tiles * splits;
-    const int64_t rounds = (units + num_cus - 1) / num_cus;
-    // Per-unit cost in 128x128x64 stage equivalents, plus a fixed overhead
-    // per unit (prologue + epilogue ~ 2 stages) and per split (partials).
-    const double stages = (double)kchunk / 64.0;
-    const double area = (double)ts.bm * ts.bn / (128.0 * 128.0);
-    const double eff = (ts.bm * ts.bn >= 256 * 128) ? 0.9 : (ts.bm * ts.bn <= 64 * 128 ? 1.25 : 1.0);
-    const double cost = (double)rounds * (area * eff * stages + 2.0 + (splits > 1 ? 1.0 : 0.0));
-    if (cost < best * 0.999) {
-      best = cost;
-      pl.tile = cands[ci];
-      pl.tiles_m = (int)tm;
-      pl.tiles_n = (int)tn;
-      pl.splits = (int)splits;
-      pl.kchunk = (int)kchunk;
+    const int64_t max_splits = forced_splits > 0 ? forced_splits : (pl.transb ? 1 : 8);
+    for (int64_t want = forced_splits > 0 ? forced_splits : 1; want <= max_splits; want *= 2) {
+      int64_t kchunk = ((K + want - 1) / want + 63) / 64 * 64;
+      const int64_t splits = (K + kchunk - 1) / kchunk;
+      if (splits > 1 && kchunk < 256 && forced_splits <= 0) break;  // keep >= 4 stages per split
+      const int64_t units = tiles * splits;
+      const int64_t rounds = (units + num_cus - 1) / num_cus;
+      double cost = (double)rounds * (kTileFixedUs + (double)kchunk / 64.0 * stage_us(cands[ci]));
+      if (splits > 1)
+        cost += kLaunchUs + (double)(splits * 4 + 2) * (double)M * (double)N / (kReduceGBs * 1e3);
+      if (cost < best * 0.999) {
+        best = cost;
+        pl.tile = cands[ci];
+        pl.tiles_m = (int)tm;
+        pl.tiles_n = (int)tn;
+        pl.splits = (int)splits;
+        pl.kchunk = (int)kchunk;
+      }
+      if (forced_splits > 0) break;
     }
   }
   if (pl.splits > 1) pl.ws_floats = (size_t)pl.splits * (size_t)M * (size_t)N;

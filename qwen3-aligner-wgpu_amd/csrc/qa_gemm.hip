@@ -437,34 +437,57 @@ __global__ void __launch_bounds__(NT * KG) gemm_dma_kernel(const GemmParams p) {
     }
   }
 
-  if constexpr (KG > 1) {
-    // Sum the k-groups' partials: groups 1.. park theirs in LDS (lane-major,
-    // conflict-free), group 0 adds them in group order.
-    constexpr int R = FM * FN * 16;  // accumulator registers per lane
-    float* red = reinterpret_cast<float*>(smem);
-    __syncthreads();  // every wave is past its last LDS read of the stages
-    if (kg > 0) {
+  // Epilogue through LDS.  The accumulators (in MFMA lane order: one token,
+  // 4-column runs) are parked as an f32 [BM][BN] tile, the k-groups summed
+  // into it in group order, and the tile leaves row by row: consecutive
+  // threads take consecutive 4-column groups, so bias / residual reads and
+  // the 16-bit stores are contiguous row segments.  Rows are padded by 4
+  // floats, which puts the 16 rows a quarter-wave writes on distinct banks.
+  constexpr int LDT = BN + 4;
+  static_assert(BM * LDT * 4 <= SMEM, "epilogue staging tile");
+  float* tile = reinterpret_cast<float*>(smem);
+  __syncthreads();  // all stages consumed (every DMA was waited for)
+#pragma unroll
+  for (int g = 0; g < KG; ++g) {
+    if (kg == g) {
 #pragma unroll
       for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
         for (int fn = 0; fn < FN; ++fn)
 #pragma unroll
-          for (int r = 0; r < 16; ++r)
-            red[(((kg - 1) * 4 + w4) * R + (fm * FN + fn) * 16 + r) * 64 + lane] = acc[fm][fn][r];
+          for (int q = 0; q < 4; ++q) {
+            const int row = wm * WTM + fm * 32 + fr;
+            const int col = n_subtile<BN, FN, EPI>(wn, fn) * 32 + 8 * q + 4 * fh;
+            f32x4* dst = reinterpret_cast<f32x4*>(tile + row * LDT + col);
+            const f32x4 v = {acc[fm][fn][4 * q], acc[fm][fn][4 * q + 1], acc[fm][fn][4 * q + 2],
+                             acc[fm][fn][4 * q + 3]};
+            *dst = (g == 0) ? v : *dst + v;
+          }
     }
     __syncthreads();
-    if (kg > 0) return;
-#pragma unroll
-    for (int g = 1; g < KG; ++g)
-#pragma unroll
-      for (int fm = 0; fm < FM; ++fm)
-#pragma unroll
-        for (int fn = 0; fn < FN; ++fn)
-#pragma unroll
-          for (int r = 0; r < 16; ++r)
-            acc[fm][fn][r] += red[(((g - 1) * 4 + w4) * R + (fm * FN + fn) * 16 + r) * 64 + lane];
   }
-  finish_tile<DT, BM, BN, EPI, FM, FN, WTM>(p, acc, C, tm, tn, split, wm, wn, fr, fh);
+  constexpr int OUTC = EPI == EPI_SILU ? BN / 2 : BN;  // output columns of the tile
+  constexpr int GPR = OUTC / 4;                          // 4-column groups per row
+  const int nfull = EPI == EPI_SILU ? p.N / 2 : p.N;
+  const int n0 = tn * OUTC;
+  for (int idx = tid; idx < BM * GPR; idx += NTH) {
+    const int r = idx / GPR, c4 = (idx % GPR) * 4;
+    const int m = m0 + r, n = n0 + c4;
+    if (m >= p.M || n >= nfull) continue;
+    const f32x4 v4 = *reinterpret_cast<const f32x4*>(tile + r * LDT + c4);
+    f32x4 u4 = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (EPI == EPI_SILU) u4 = *reinterpret_cast<const f32x4*>(tile + r * LDT + BN / 2 + c4);
+    if (p.splits > 1) {
+      f32x4* ws = reinterpret_cast<f32x4*>(p.ws);
+      const int64_t rowbase = ((int64_t)split * p.M + m) * p.N;
+      ws[(rowbase + n) >> 2] = v4;
+      if constexpr (EPI == EPI_SILU) ws[(rowbase + nfull + n) >> 2] = u4;
+      continue;
+    }
+    const float v[4] = {v4.x, v4.y, v4.z, v4.w};
+    const float uu[4] = {u4.x, u4.y, u4.z, u4.w};
+    epilogue4<DT, EPI>(p, C, m, n, v, uu);
+  }
 }
 
 // W as [K, N] (row stride ldb): register-staged, double-buffered; each
@@ -652,6 +675,10 @@ hipError_t launch_epi(const Plan& plan, const GemmParams& p, int batch, hipStrea
       case TILE_256x128: e = launch_dma<DT, 256, 128, 3, EPI, 2>(plan, p, batch, s); break;
       case TILE_128x256: e = launch_dma<DT, 128, 256, 3, EPI, 2>(plan, p, batch, s); break;
       case TILE_64x128: e = launch_dma<DT, 64, 128, 4, EPI, 2>(plan, p, batch, s); break;
+      case TILE_64x64:
+        if constexpr (EPI == EPI_SILU) return hipErrorInvalidValue;  // never planned
+        else e = launch_dma<DT, 64, 64, 4, EPI, 2>(plan, p, batch, s);
+        break;
       default: e = launch_dma<DT, 128, 128, 4, EPI, 2>(plan, p, batch, s); break;
     }
   }

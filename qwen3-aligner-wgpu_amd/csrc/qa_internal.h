@@ -14,12 +14,14 @@ namespace qa {
 // GELU and SiLU-mul change the epilogue's arithmetic and its column mapping.
 enum Epi : int { EPI_PLAIN = 0, EPI_GELU = 1, EPI_SILU = 2 };
 
-// Tile shapes (block BM x BN, 4 waves).  Chosen per call by plan_linear().
+// Tile shapes (block BM x BN; two k-groups of 2x2 waves each).  Chosen per
+// call by plan_linear().
 enum TileCfg : int {
-  TILE_128x128 = 0,  // 2x2 waves of 64x64
-  TILE_256x128 = 1,  // 2x2 waves of 128(m) x 64(n)
-  TILE_128x256 = 2,  // 2x2 waves of 64(m) x 128(n)
-  TILE_64x128 = 3,   // 2x2 waves of 32(m) x 64(n)
+  TILE_128x128 = 0,  // waves of 64x64
+  TILE_256x128 = 1,  // waves of 128(m) x 64(n)
+  TILE_128x256 = 2,  // waves of 64(m) x 128(n)
+  TILE_64x128 = 3,   // waves of 32(m) x 64(n)
+  TILE_64x64 = 4,    // waves of 32x32 (not for SiLU-mul, which pairs 2 subtiles)
   TILE_COUNT
 };
 
@@ -31,6 +33,7 @@ inline TileShape tile_shape(int cfg) {
     case TILE_256x128: return {256, 128};
     case TILE_128x256: return {128, 256};
     case TILE_64x128: return {64, 128};
+    case TILE_64x64: return {64, 64};
     default: return {128, 128};
   }
 }

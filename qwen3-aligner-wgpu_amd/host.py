@@ -31,7 +31,7 @@ def declare(L: ctypes.CDLL) -> None:
     L.qah_decoder_set_inputs.argtypes = [_vp, _i, _vp, _vp, _vp, _vp]
     L.qah_decoder_prefill_linears.argtypes = [_vp, _i]
     L.qah_decoder_read.argtypes = [_vp, _i, _i, _vp]
-    L.qah_decoder_time.argtypes = [_vp, _i, _i, _i, _i, _dp]
+    L.qah_decoder_time.argtypes = [_vp, _i, _i, _i, _i, _dp, _dp]
     L.qah_decoder_profile_sites.argtypes = [_vp, _i, _i, _dp]
     L.qah_decoder_destroy.argtypes = [_vp]
     L.qah_decoder_destroy.restype = None
@@ -41,7 +41,7 @@ def declare(L: ctypes.CDLL) -> None:
     L.qah_encoder_set_inputs.argtypes = [_vp, _i, _vp, _vp, _vp, _vp, _vp]
     L.qah_encoder_forward_linears.argtypes = [_vp, _i]
     L.qah_encoder_read.argtypes = [_vp, _i, _i, _vp]
-    L.qah_encoder_time.argtypes = [_vp, _i, _i, _i, _i, _dp]
+    L.qah_encoder_time.argtypes = [_vp, _i, _i, _i, _i, _dp, _dp]
     L.qah_encoder_profile_sites.argtypes = [_vp, _i, _i, _dp]
     L.qah_encoder_destroy.argtypes = [_vp]
     L.qah_encoder_destroy.restype = None
@@ -127,11 +127,12 @@ class DecoderLinears:
         check(host_lib().qah_decoder_read(self.handle, idx, rows, out.ctypes.data))
         return out
 
-    def time(self, rows, warmup, steps, use_graph=True) -> float:
-        ms = ctypes.c_double()
+    def time(self, rows, warmup, steps, use_graph=True) -> tuple[float, float]:
+        """(event ms per step, host wall-clock ms per step)."""
+        ms, wall = ctypes.c_double(), ctypes.c_double()
         check(host_lib().qah_decoder_time(self.handle, rows, warmup, steps, int(use_graph),
-                                          ctypes.byref(ms)))
-        return ms.value
+                                          ctypes.byref(ms), ctypes.byref(wall)))
+        return ms.value, wall.value
 
     def profile_sites(self, rows, steps) -> dict:
         out = (ctypes.c_double * 4)()
@@ -180,11 +181,12 @@ class EncoderLinears:
         check(host_lib().qah_encoder_read(self.handle, idx, rows, out.ctypes.data))
         return out
 
-    def time(self, rows, warmup, steps, use_graph=True) -> float:
-        ms = ctypes.c_double()
+    def time(self, rows, warmup, steps, use_graph=True) -> tuple[float, float]:
+        """(event ms per step, host wall-clock ms per step)."""
+        ms, wall = ctypes.c_double(), ctypes.c_double()
         check(host_lib().qah_encoder_time(self.handle, rows, warmup, steps, int(use_graph),
-                                          ctypes.byref(ms)))
-        return ms.value
+                                          ctypes.byref(ms), ctypes.byref(wall)))
+        return ms.value, wall.value
 
     def profile_sites(self, rows, steps) -> dict:
         out = (ctypes.c_double * 5)()

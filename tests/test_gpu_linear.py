@@ -153,7 +153,7 @@ def test_batched(ctx, pkg, orc, dtype):
     assert_parity(got.reshape(batch, m, n), want, orc, dtype, ulp_tol=1)
 
 
-@pytest.mark.parametrize("tile", [0, 1, 2, 3])
+@pytest.mark.parametrize("tile", [0, 1, 2, 3, 4])
 @pytest.mark.parametrize("splits", [1, 2, 3, 5])
 def test_forced_tiles_and_splits(ctx, pkg, orc, tile, splits):
     """Every tile shape, with and without split-K (incl. uneven k ranges)."""
