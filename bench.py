@@ -42,6 +42,19 @@ METRIC = "GEMM TFLOP/s + % MFMA peak (f16, M=1024); aligner forward ms per 300 s
 
 DEC = dict(layers=28, hidden=1024, q_dim=2048, kv_dim=1024, inter=3072)
 ENC = dict(layers=18, d_model=896, ffn=3584, conv_k=128 * 9)
+COPY_CAL_BYTES = 512 << 20
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemm_decoder_config3_traffic.json")
+
+
+def measured_traffic(site: str):
+    """HBM-side bytes per launch of a site's kernel, from the committed
+    FETCH_SIZE / WRITE_SIZE passes (scaled by the copy calibration), or None."""
+    try:
+        prof = json.load(open(TRAFFIC_PROFILE))
+        entry = prof["sites"][site]
+        return int(entry["traffic_bytes"]), entry["kernel"]
+    except (OSError, KeyError, ValueError):
+        return None, None
 
 
 def log(*a):
@@ -149,6 +162,8 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=12.0,
                     help="seconds of oracle work for cpu_baseline (0 disables)")
     ap.add_argument("--no-detail", action="store_true", help="skip configs 1, 2, 4")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain 512 MiB copy 3 times (calibrates FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -160,6 +175,12 @@ def main():
 
     pkg = entry.load_package()
     from qwen3_aligner_wgpu_amd import host
+
+    if args.copy_calibration:
+        with pkg.Context(0) as ctx:
+            host.copy_calibration(ctx, COPY_CAL_BYTES, 3)
+        log(f"[bench] copied {COPY_CAL_BYTES} bytes x3")
+        return
 
     m = 1024
     ctx = pkg.Context(0)
@@ -213,6 +234,7 @@ def main():
         detail["config4_sites_us"] = {k: round(v * 1e3, 2) for k, v in sites4.items()}
     ctx.close()
 
+    traffic, traffic_kernel = measured_traffic("gu")
     cpu = None
     if args.cpu_budget > 0:
         orc = entry.load_oracle()
@@ -250,7 +272,9 @@ def main():
             "peak": PEAK_F16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_F16_TFLOPS, 4),
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_kernel": traffic_kernel,
+            "traffic_source": "profiles/gemm_decoder_config3_traffic.md" if traffic else None,
         },
         "cpu_baseline": cpu,
         "detail": detail,

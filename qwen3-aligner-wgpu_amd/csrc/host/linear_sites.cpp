@@ -379,6 +379,12 @@ struct qah_encoder {
 
 namespace {
 
+__global__ void copy_kernel(const uint4* __restrict__ src, uint4* __restrict__ dst, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x)
+    dst[i] = src[i];
+}
+
 // Runs `step` warmup + steps times; optional graph capture of one step.
 template <class Step>
 int time_steps(qa_ctx* ctx, int warmup, int steps, int use_graph, Step&& step, double* ms,
@@ -612,6 +618,25 @@ int qah_time_linear(qa_ctx* ctx, const qa_linear_desc* desc, int warmup, int ite
                     double* ms_per_launch) {
   if (!ctx || !desc || !ms_per_launch) return QA_EINVAL;
   return time_steps(ctx, warmup, iters, 0, [&] { return qa_linear(ctx, desc); }, ms_per_launch);
+}
+
+int qah_copy_calibration(qa_ctx* ctx, size_t bytes, int reps) {
+  if (!ctx || bytes % 16 || reps <= 0) return QA_EINVAL;
+  Buffer a, b;
+  int rc = alloc(ctx, bytes, &a);
+  if (rc == QA_OK) rc = alloc(ctx, bytes, &b);
+  hipStream_t s = (hipStream_t)qa_ctx_stream(ctx);
+  if (rc == QA_OK) rc = hip_status(hipMemsetAsync(a.ptr, 1, bytes, s));
+  if (rc == QA_OK) rc = qa_sync(ctx);
+  for (int i = 0; i < reps && rc == QA_OK; ++i) {
+    hipLaunchKernelGGL(copy_kernel, dim3(8192), dim3(256), 0, s, (const uint4*)a.ptr, (uint4*)b.ptr,
+                       bytes / 16);
+    rc = hip_status(hipGetLastError());
+  }
+  if (rc == QA_OK) rc = qa_sync(ctx);
+  release(ctx, &a);
+  release(ctx, &b);
+  return rc;
 }
 
 }  // extern "C"

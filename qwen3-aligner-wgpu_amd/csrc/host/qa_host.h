@@ -112,6 +112,11 @@ void qah_encoder_destroy(qah_encoder* e);
 int qah_time_linear(qa_ctx* ctx, const qa_linear_desc* desc, int warmup, int iters,
                     double* ms_per_launch);
 
+/* A plain 16-byte-per-thread copy of `bytes` between two fresh buffers,
+ * `reps` times: the known-size reference that calibrates the FETCH_SIZE /
+ * WRITE_SIZE counters. */
+int qah_copy_calibration(qa_ctx* ctx, size_t bytes, int reps);
+
 #ifdef __cplusplus
 }
 #endif

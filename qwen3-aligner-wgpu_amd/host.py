@@ -46,12 +46,13 @@ def declare(L: ctypes.CDLL) -> None:
     L.qah_encoder_destroy.argtypes = [_vp]
     L.qah_encoder_destroy.restype = None
     L.qah_time_linear.argtypes = [_vp, _vp, _i, _i, _dp]
+    L.qah_copy_calibration.argtypes = [_vp, _sz, _i]
     for name in ("qah_decoder_create", "qah_decoder_load_layer", "qah_decoder_set_inputs",
                  "qah_decoder_prefill_linears", "qah_decoder_read", "qah_decoder_time",
                  "qah_decoder_profile_sites", "qah_encoder_create", "qah_encoder_load_layer",
                  "qah_encoder_load_conv", "qah_encoder_set_inputs", "qah_encoder_forward_linears",
                  "qah_encoder_read", "qah_encoder_time", "qah_encoder_profile_sites",
-                 "qah_time_linear"):
+                 "qah_time_linear", "qah_copy_calibration"):
         getattr(L, name).restype = _i
 
 
@@ -199,3 +200,8 @@ def time_linear(ctx, desc, warmup: int, iters: int) -> float:
     check(host_lib().qah_time_linear(ctx.handle, ctypes.byref(desc), warmup, iters,
                                      ctypes.byref(ms)))
     return ms.value
+
+
+def copy_calibration(ctx, nbytes: int, reps: int = 3) -> None:
+    """qah_copy_calibration: a plain copy of nbytes, reps times (counter calibration)."""
+    check(host_lib().qah_copy_calibration(ctx.handle, nbytes, reps))
