@@ -135,10 +135,11 @@ int validate(const qa_linear_desc* d) {
 double stage_us(int tile) {
   switch (tile) {
     case qa::TILE_256x128:
-    case qa::TILE_128x256: return 1.10;
-    case qa::TILE_64x128: return 0.34;
-    case qa::TILE_64x64: return 0.26;
-    default: return 0.60;
+    case qa::TILE_128x256: return 0.95;
+    case qa::TILE_128x192: return 0.72;
+    case qa::TILE_64x128: return 0.36;
+    case qa::TILE_64x64: return 0.27;
+    default: return 0.56;
   }
 }
 constexpr double kTileFixedUs = 3.0;
@@ -161,11 +162,10 @@ qa::Plan plan_linear(const qa_linear_desc& d, int num_cus) {
   if (const char* e = getenv("QA_SPLITS")) forced_splits = atoi(e);
 
   int cands[qa::TILE_COUNT] = {qa::TILE_128x128, qa::TILE_256x128, qa::TILE_128x256,
-                               qa::TILE_64x128, qa::TILE_64x64};
-  int ncand = silu ? qa::TILE_COUNT - 1 : qa::TILE_COUNT;  // 64x64 cannot pair gate/up
+                               qa::TILE_64x128,  qa::TILE_64x64,   qa::TILE_128x192};
+  int ncand = qa::TILE_COUNT;
   if (pl.transb) ncand = 1;  // the conv operand path has one tile shape
-  if (forced_tile >= 0 && forced_tile < qa::TILE_COUNT && !pl.transb &&
-      !(silu && forced_tile == qa::TILE_64x64)) {
+  if (forced_tile >= 0 && forced_tile < qa::TILE_COUNT && !pl.transb) {
     cands[0] = forced_tile;
     ncand = 1;
   }

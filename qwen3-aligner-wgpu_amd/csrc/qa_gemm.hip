@@ -112,6 +112,13 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
+// s_waitcnt lgkmcnt(0): this wave's LDS reads have returned.  The scheduling
+// barrier keeps earlier MFMAs from sinking below the wait.
+__device__ __forceinline__ void wait_lds() {
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_waitcnt(0xF | (0x3 << 14) | (0x7 << 4) | (0x0 << 8));
+}
+
 // Workgroup execution barrier with no memory fence; the asm statements keep
 // the compiler from moving LDS accesses across it.
 __device__ __forceinline__ void exec_barrier() {
@@ -301,7 +308,7 @@ __global__ void __launch_bounds__(NT * KG) gemm_dma_kernel(const GemmParams p) {
   static_assert(KG == 1 || KG == 2 || KG == 4, "k groups");
   static_assert(FM >= 1 && FN >= 1 && AJ >= 1 && BJ >= 1, "tile shape");
   static_assert(BM % (8 * NW) == 0 && BN % (8 * NW) == 0, "DMA row groups");
-  static_assert(EPI != EPI_SILU || FN % 2 == 0, "SiLU pairs gate/up subtiles per wave");
+  static_assert(EPI != EPI_SILU || BN % 64 == 0, "SiLU tiles hold whole gate / up subtiles");
   static_assert(S >= 2 && (S - 1) * LPS < 64, "pipeline depth");
   static_assert(KG == 1 || (KG - 1) * 4 * BM * BN <= SMEM, "reduction buffer");
   __shared__ __attribute__((aligned(1024))) unsigned char smem[SMEM];
@@ -386,7 +393,7 @@ __global__ void __launch_bounds__(NT * KG) gemm_dma_kernel(const GemmParams p) {
     const int c = kk * 2 + fh;
 #pragma unroll
     for (int fn = 0; fn < FN; ++fn) {
-      const int row = n_subtile<BN, FN, EPI>(wn, fn) * 32 + fr;
+      const int row = (wn * FN + fn) * 32 + fr;
       fa[slot][fn] = *reinterpret_cast<const u32x4*>(sB + row * 128 + ((c ^ swz(row)) << 4));
     }
 #pragma unroll
@@ -404,9 +411,13 @@ __global__ void __launch_bounds__(NT * KG) gemm_dma_kernel(const GemmParams p) {
   };
 
   // Pipeline: all S buffers are filled up front; the fragments of the next
-  // slice are read while the current one multiplies; the barrier that
-  // publishes stage it+1 (and frees stage it's buffer for stage it+S) comes
-  // after the stage's last MFMAs are issued, so it overlaps matrix-core work.
+  // slice are read while the current one multiplies.  The barrier that
+  // publishes stage it+1 (and frees stage it's buffer for stage it+S) sits
+  // before the stage's last slice is multiplied: each wave first waits for
+  // its own reads of the stage (all of them issued by then), and after the
+  // barrier the first fragments of stage it+1 load while the last slice's
+  // MFMAs run, so no wave stalls on LDS right after the barrier.
+  static_assert(SPG % 2 == 0, "fragment slots alternate within a stage");
   const int kk0 = kg * SPG;
   if (nk > 0) {
 #pragma unroll
@@ -421,10 +432,11 @@ __global__ void __launch_bounds__(NT * KG) gemm_dma_kernel(const GemmParams p) {
     for (int it = 0; it < nk; ++it) {
       const int buf = it % S;
 #pragma unroll
-      for (int q = 0; q < SPG; ++q) {
-        if (q + 1 < SPG) read_frags(buf, kk0 + q + 1, (q + 1) & 1);
+      for (int q = 0; q + 1 < SPG; ++q) {
+        read_frags(buf, kk0 + q + 1, (q + 1) & 1);
         mma(q & 1);
       }
+      wait_lds();  // unconditional: both paths reach the last MFMAs with ready slots
       if (it + 1 < nk) {
         if (it + S - 1 < nk)
           wait_vmcnt<(S - 2) * LPS>();
@@ -434,6 +446,7 @@ __global__ void __launch_bounds__(NT * KG) gemm_dma_kernel(const GemmParams p) {
         if (it + S < nk) issue(it + S, buf);
         read_frags((it + 1) % S, kk0, 0);
       }
+      mma((SPG - 1) & 1);
     }
   }
 
@@ -457,7 +470,7 @@ __global__ void __launch_bounds__(NT * KG) gemm_dma_kernel(const GemmParams p) {
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
             const int row = wm * WTM + fm * 32 + fr;
-            const int col = n_subtile<BN, FN, EPI>(wn, fn) * 32 + 8 * q + 4 * fh;
+            const int col = (wn * FN + fn) * 32 + 8 * q + 4 * fh;
             f32x4* dst = reinterpret_cast<f32x4*>(tile + row * LDT + col);
             const f32x4 v = {acc[fm][fn][4 * q], acc[fm][fn][4 * q + 1], acc[fm][fn][4 * q + 2],
                              acc[fm][fn][4 * q + 3]};
@@ -675,10 +688,8 @@ hipError_t launch_epi(const Plan& plan, const GemmParams& p, int batch, hipStrea
       case TILE_256x128: e = launch_dma<DT, 256, 128, 3, EPI, 2>(plan, p, batch, s); break;
       case TILE_128x256: e = launch_dma<DT, 128, 256, 3, EPI, 2>(plan, p, batch, s); break;
       case TILE_64x128: e = launch_dma<DT, 64, 128, 4, EPI, 2>(plan, p, batch, s); break;
-      case TILE_64x64:
-        if constexpr (EPI == EPI_SILU) return hipErrorInvalidValue;  // never planned
-        else e = launch_dma<DT, 64, 64, 4, EPI, 2>(plan, p, batch, s);
-        break;
+      case TILE_64x64: e = launch_dma<DT, 64, 64, 4, EPI, 2>(plan, p, batch, s); break;
+      case TILE_128x192: e = launch_dma<DT, 128, 192, 4, EPI, 2>(plan, p, batch, s); break;
       default: e = launch_dma<DT, 128, 128, 4, EPI, 2>(plan, p, batch, s); break;
     }
   }

@@ -21,7 +21,8 @@ enum TileCfg : int {
   TILE_256x128 = 1,  // waves of 128(m) x 64(n)
   TILE_128x256 = 2,  // waves of 64(m) x 128(n)
   TILE_64x128 = 3,   // waves of 32(m) x 64(n)
-  TILE_64x64 = 4,    // waves of 32x32 (not for SiLU-mul, which pairs 2 subtiles)
+  TILE_64x64 = 4,    // waves of 32x32
+  TILE_128x192 = 5,  // waves of 64(m) x 96(n)
   TILE_COUNT
 };
 
@@ -34,6 +35,7 @@ inline TileShape tile_shape(int cfg) {
     case TILE_128x256: return {128, 256};
     case TILE_64x128: return {64, 128};
     case TILE_64x64: return {64, 64};
+    case TILE_128x192: return {128, 192};
     default: return {128, 128};
   }
 }

@@ -89,3 +89,59 @@ def assert_parity(got_bits, want_bits, orc, dtype, rel_tol=REL_TOL, mae_tol=MAE_
     if ulp_tol is not None:
         assert s["max_ulp"] <= ulp_tol, s
     return s
+
+
+def ulp16(x: np.ndarray, dtype: int) -> np.ndarray:
+    """Spacing of the 16-bit format (f16 or bf16) at |x|, in float64."""
+    mant, emin = (10, -14) if dtype == 0 else (7, -126)
+    ax = np.abs(np.asarray(x, np.float64))
+    e = np.floor(np.log2(np.where(ax > 0, ax, 1.0)))
+    e = np.maximum(np.where(ax > 0, e, emin), emin)
+    return np.exp2(e - mant)
+
+
+def silu_mul_bound(a_bits, w_bits, gu_exact_bits, want_bits, orc, dtype, k):
+    """Elementwise bound on |act_gpu - act_exact| for act = r(silu(r(g)) * r(u)).
+
+    The GPU's rounded g and u (r = 16-bit RNE) are each within one ulp of the
+    exactly rounded value plus the f32 accumulation error of its sum, at most
+    (K/16 + 2) * 2^-24 * sum_k |a_k w_k|: each 32x32x16 MFMA adds 16 exact
+    f16/bf16 products into the f32 accumulator (K/16 accumulations along a
+    k chain, counting the k-group merge), the classic gamma_n bound.  That
+    perturbation propagates through silu(g) * u with the first-order terms
+    |silu'(g) u| dg and |silu(g)| du, the cross term max|silu'| dg du
+    (silu' <= 1.1) and the curvature term max|silu''| dg^2 |u| / 2
+    (silu'' <= 0.5); the final rounding adds one ulp of the result, and the
+    f32 evaluation of silu a few f32 ulps (1e-6 relative)."""
+    n = gu_exact_bits.shape[1] // 2
+    gu = orc.h16_to_f32(gu_exact_bits, dtype).astype(np.float64)
+    g, u = gu[:, :n], gu[:, n:]
+    af = np.abs(orc.h16_to_f32(a_bits, dtype).astype(np.float64))
+    wf = np.abs(orc.h16_to_f32(w_bits, dtype).astype(np.float64))
+    sabs = af @ wf.T
+    eps = (k / 16.0 + 2.0) * 2.0 ** -24 * sabs
+    dg = ulp16(g, dtype) + eps[:, :n]
+    du = ulp16(u, dtype) + eps[:, n:]
+    sig = 1.0 / (1.0 + np.exp(-g))
+    silu = g * sig
+    dsilu = sig * (1.0 + g * (1.0 - sig))
+    want = orc.h16_to_f32(want_bits, dtype).astype(np.float64)
+    return (np.abs(dsilu * u) * dg + (np.abs(silu) + 1.1 * dg) * du + 0.25 * dg * dg * np.abs(u)
+            + ulp16(want, dtype) + 1e-6 * np.abs(silu * u))
+
+
+def assert_silu_mul(got_bits, want_bits, a_bits, w_bits, gu_exact_bits, orc, dtype, k,
+                    rel_tol=REL_TOL, min_identical=0.97):
+    """SiLU.up output against the exactly rounded reference: the north-star
+    statistics, the propagated-rounding bound elementwise, and a floor on the
+    share of bit-identical outputs (differences come only from rounding ties
+    the f32 summation order moves, a small share)."""
+    s = assert_parity(got_bits, want_bits, orc, dtype, rel_tol=rel_tol)
+    bound = silu_mul_bound(a_bits, w_bits, gu_exact_bits, want_bits, orc, dtype, k)
+    got = orc.h16_to_f32(got_bits, dtype).astype(np.float64)
+    want = orc.h16_to_f32(want_bits, dtype).astype(np.float64)
+    excess = np.abs(got - want) - bound
+    worst = np.unravel_index(np.argmax(excess), excess.shape)
+    assert excess.max() <= 0, (s, worst, got[worst], want[worst], bound[worst])
+    assert s["identical"] >= min_identical, s
+    return s
