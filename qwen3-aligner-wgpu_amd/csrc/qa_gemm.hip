@@ -443,10 +443,15 @@ __global__ void __launch_bounds__(NT * KG) gemm_dma_kernel(const GemmParams p) {
         else
           wait_vmcnt<0>();
         exec_barrier();
-        if (it + S < nk) issue(it + S, buf);
         read_frags((it + 1) % S, kk0, 0);
       }
       mma((SPG - 1) & 1);
+      // Refill the freed buffer behind this wave's LDS reads and MFMAs (issued
+      // ahead of them, the DMA writes measurably delay the fragment reads).
+      if (it + 1 < nk && it + S < nk) {
+        __builtin_amdgcn_sched_barrier(0);
+        issue(it + S, buf);
+      }
     }
   }
 
@@ -690,7 +695,7 @@ hipError_t launch_epi(const Plan& plan, const GemmParams& p, int batch, hipStrea
       case TILE_64x128: e = launch_dma<DT, 64, 128, 4, EPI, 2>(plan, p, batch, s); break;
       case TILE_64x64: e = launch_dma<DT, 64, 64, 4, EPI, 2>(plan, p, batch, s); break;
       case TILE_128x192: e = launch_dma<DT, 128, 192, 4, EPI, 2>(plan, p, batch, s); break;
-      default: e = launch_dma<DT, 128, 128, 4, EPI, 2>(plan, p, batch, s); break;
+      default: e = launch_dma<DT, 128, 128, 5, EPI, 2>(plan, p, batch, s); break;
     }
   }
   if (e != hipSuccess || plan.splits == 1) return e;
