@@ -197,6 +197,25 @@ qa::Plan plan_linear(const qa_linear_desc& d, int num_cus) {
     }
   }
   if (pl.splits > 1) pl.ws_floats = (size_t)pl.splits * (size_t)M * (size_t)N;
+
+  // XCD rectangles: operand rows each XCD's L2 must fetch, M/g of A plus
+  // N/(8/g) of W for a g x (8/g) grid (g = 1: all of A, 1/8 of W); the grid
+  // must divide the tile grid.  QA_XCD_GM forces g when it does.
+  pl.xcd_gm = 1;
+  if (!pl.transb) {
+    int forced_g = 0;
+    if (const char* e = getenv("QA_XCD_GM")) forced_g = atoi(e);
+    double best_rows = (double)M + (double)N / 8.0;
+    for (int g = 2; g <= 8; g *= 2) {
+      if (pl.tiles_m % g != 0 || pl.tiles_n % (8 / g) != 0) continue;
+      const double rows = (double)M / g + (double)N / (8 / g);
+      if (forced_g == g || (forced_g == 0 && rows < best_rows * 0.999)) {
+        best_rows = rows;
+        pl.xcd_gm = g;
+      }
+    }
+    if (forced_g == 1) pl.xcd_gm = 1;
+  }
   return pl;
 }
 
@@ -357,6 +376,7 @@ int qa_linear(qa_ctx* ctx, const qa_linear_desc* d) {
   p.kchunk = plan.kchunk;
   p.accumulate = (d->flags & QA_ACCUMULATE) ? 1 : 0;
   p.bias_rows = (d->flags & QA_BIAS_ROWS) ? 1 : 0;
+  p.xcd_gm = plan.xcd_gm;
   const int batch = d->batch > 0 ? (int)d->batch : 1;
   if (plan.splits > 1 && batch > 1)
     return fail(QA_EUNSUPPORTED, "qa_linear: split-K with batch > 1");

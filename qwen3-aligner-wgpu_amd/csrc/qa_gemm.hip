@@ -28,7 +28,8 @@
 //    answers with zeros: ragged edges cost nothing and need no padding.
 //  * XCD-aware block order: the hardware deals workgroups round-robin over
 //    the 8 XCDs; units are renumbered so each XCD gets a contiguous range of
-//    tiles (whole n-blocks of W), keeping each weight slice in one L2.
+//    whole n-blocks of W, or (tile_of, xcd_gm > 1) a rectangle of the tile
+//    grid, whichever makes its L2 fetch fewer operand rows.
 //  * Split-K: each split writes f32 partials; splitk_reduce_kernel sums them
 //    in split order (deterministic) and runs the epilogue.
 //
@@ -105,6 +106,34 @@ __device__ __forceinline__ int xcd_remap(int b, int n) {
   return (b % X) * per + b / X;
 }
 
+// Block -> (tile m, tile n, k split).  Workgroups are dealt round-robin over
+// the 8 XCDs (block b runs on XCD b % 8), each with its own L2.  With
+// xcd_gm = g > 1 the tile grid is cut into a g x (8/g) grid of rectangles,
+// one per XCD, so an XCD's L2 holds M/g rows of A and N/(8/g) rows of W
+// instead of all of A; otherwise each XCD takes a contiguous range of whole
+// n-blocks (all of A, 1/8 of W).  The planner sets g only when it divides the
+// tile grid.  Within a rectangle, m runs fastest and the k splits of a tile
+// are adjacent.
+__device__ __forceinline__ void tile_of(const GemmParams& p, int b, int& tm, int& tn,
+                                        int& split) {
+  constexpr int X = 8;
+  const int g = p.xcd_gm;
+  if (g > 1) {
+    const int rm = p.tiles_m / g, rn = p.tiles_n / (X / g);
+    const int xcd = b % X, l = b / X;
+    const int t = l / p.splits;
+    split = l % p.splits;
+    tm = (xcd % g) * rm + t % rm;
+    tn = (xcd / g) * rn + t / rm;
+    return;
+  }
+  const int u = xcd_remap(b, p.tiles_m * p.tiles_n * p.splits);
+  split = u % p.splits;
+  const int t = u / p.splits;
+  tn = t / p.tiles_m;
+  tm = t % p.tiles_m;
+}
+
 // s_waitcnt vmcnt(N) leaving expcnt / lgkmcnt unconstrained (gfx9 encoding).
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -129,11 +158,34 @@ __device__ __forceinline__ void exec_barrier() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
+// The epilogue math runs on the hardware transcendentals (v_exp_f32 = 2^x,
+// v_rcp_f32 = 1/x, about 1 f32 ulp each): a full-precision expf / erff and an
+// IEEE divide cost ~30-40 VALU instructions per output, which made the
+// SiLU.up epilogue a quarter of the gate|up kernel.  Either error is a few f32
+// ulps, far below the 16-bit rounding that follows.
+constexpr float kLog2e = 1.44269504088896341f;
+
+// erf GELU, 0.5 x (1 + erf(x / sqrt 2)) (src/audio_encoder.rs:196-202), with
+// erf from Abramowitz & Stegun 7.1.26 (|error| <= 1.5e-7; the reference's GPU
+// path uses the same approximation, src/shaders.rs:2593-2625):
+//   erf(a) = 1 - P(t) e^{-a^2},  t = 1 / (1 + 0.3275911 a),  a >= 0.
+// For x < 0 the factor 1 + erf(x / sqrt 2) = P(t) e^{-a^2} is formed directly,
+// without cancelling against 1.
 __device__ __forceinline__ float gelu_erf(float x) {
-  return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f));
+  const float a = fabsf(x) * 0.70710678118654752f;
+  const float t = __builtin_amdgcn_rcpf(1.0f + 0.3275911f * a);
+  const float poly =
+      ((((1.061405429f * t - 1.453152027f) * t + 1.421413741f) * t - 0.284496736f) * t +
+       0.254829592f) * t;
+  const float q = poly * __builtin_amdgcn_exp2f(-a * a * kLog2e);  // 1 - erf(a)
+  return 0.5f * x * (x >= 0.0f ? 2.0f - q : q);
 }
 
-__device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
+// g * sigmoid(g) * u with sigmoid(g) = 1 / (1 + 2^(-g log2 e)), the reference
+// GPU kernel's form (src/shaders.rs:1411-1450).
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g * kLog2e)) * u;
+}
 
 template <int DT>
 __device__ __forceinline__ void store4(uint16_t* p, const float* v) {
@@ -320,11 +372,8 @@ __global__ void __launch_bounds__(NT * KG) gemm_dma_kernel(const GemmParams p) {
   const int wm = w4 % WGM, wn = w4 / WGM;
   const int fr = lane & 31, fh = lane >> 5;  // fragment row, k-chunk parity
 
-  const int units = p.tiles_m * p.tiles_n * p.splits;
-  const int u = xcd_remap((int)blockIdx.x, units);
-  const int split = u % p.splits;
-  const int t = u / p.splits;
-  const int tn = t / p.tiles_m, tm = t % p.tiles_m;
+  int tm, tn, split;
+  tile_of(p, (int)blockIdx.x, tm, tn, split);
   const int64_t z = blockIdx.y;
   const uint16_t* A = p.a + z * p.bsa;
   const uint16_t* W = p.w + z * p.bsb;
@@ -527,11 +576,8 @@ __global__ void __launch_bounds__(NT) gemm_reg_kernel(const GemmParams p) {
   const int wm = wave % WGM, wn = wave / WGM;
   const int fr = lane & 31, fh = lane >> 5;
 
-  const int units = p.tiles_m * p.tiles_n * p.splits;
-  const int u = xcd_remap((int)blockIdx.x, units);
-  const int split = u % p.splits;
-  const int t = u / p.splits;
-  const int tn = t / p.tiles_m, tm = t % p.tiles_m;
+  int tm, tn, split;
+  tile_of(p, (int)blockIdx.x, tm, tn, split);
   const int64_t z = blockIdx.y;
   const uint16_t* __restrict__ A = p.a + z * p.bsa;
   const uint16_t* __restrict__ W = p.w + z * p.bsb;

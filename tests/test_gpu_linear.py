@@ -180,6 +180,32 @@ def test_forced_tiles_and_splits(ctx, pkg, orc, tile, splits):
     assert_silu_mul(act, act_exact, a, gu_w, gu_exact, orc, 0, k)
 
 
+@pytest.mark.parametrize("xcd_gm", [1, 2, 4, 8])
+@pytest.mark.parametrize("tile,splits", [(4, 1), (0, 1), (3, 2), (5, 1)])
+def test_xcd_tile_grids(ctx, pkg, orc, xcd_gm, tile, splits):
+    """Every XCD rectangle grid maps blocks onto tiles one to one: C starts as
+    noise and must end equal to the exactly rounded result everywhere (a tile
+    computed twice leaves another one untouched)."""
+    rng = np.random.default_rng(40 + xcd_gm + 10 * tile)
+    m, n, k = 512, 1536, 640   # 64x64: 8x24 tiles; 128x128: 4x12; 64x128: 8x12; 128x192: 4x8
+    a, w = _case(rng, orc, 0, m, n, k)
+    c0 = _h16(orc, rng.standard_normal((m, n)), 0)
+    os.environ.update(QA_TILE=str(tile), QA_SPLITS=str(splits), QA_XCD_GM=str(xcd_gm))
+    try:
+        got = _run(ctx, pkg, 0, a, w, c0)
+        gu_w = _h16(orc, 0.05 * rng.standard_normal((2 * 768, k)), 0)
+        act = _run(ctx, pkg, 0, a, gu_w, np.zeros((m, 768), np.uint16), flags=pkg.EPI_SILU_MUL)
+    finally:
+        for key in ("QA_TILE", "QA_SPLITS", "QA_XCD_GM"):
+            del os.environ[key]
+    exact = orc.linear(0, a, w, np.zeros_like(c0), flags=orc.EXACT)
+    assert_parity(got, exact, orc, 0, ulp_tol=1)
+    act_exact = orc.linear(0, a, gu_w, np.zeros((m, 768), np.uint16),
+                           flags=orc.EPI_SILU_MUL | orc.EXACT)
+    gu_exact = orc.linear(0, a, gu_w, np.zeros((m, 1536), np.uint16), flags=orc.EXACT)
+    assert_silu_mul(act, act_exact, a, gu_w, gu_exact, orc, 0, k)
+
+
 @pytest.mark.parametrize("dtype", [0, 1], ids=["f16", "bf16"])
 def test_mlp_fused_config2(ctx, pkg, orc, dtype):
     """out = down(SiLU(x Wg^T) * (x Wu^T)) + x, M=512."""
