@@ -198,23 +198,31 @@ qa::Plan plan_linear(const qa_linear_desc& d, int num_cus) {
   }
   if (pl.splits > 1) pl.ws_floats = (size_t)pl.splits * (size_t)M * (size_t)N;
 
-  // XCD rectangles: operand rows each XCD's L2 must fetch, M/g of A plus
-  // N/(8/g) of W for a g x (8/g) grid (g = 1: all of A, 1/8 of W); the grid
-  // must divide the tile grid.  QA_XCD_GM forces g when it does.
-  pl.xcd_gm = 1;
-  if (!pl.transb) {
-    int forced_g = 0;
-    if (const char* e = getenv("QA_XCD_GM")) forced_g = atoi(e);
-    double best_rows = (double)M + (double)N / 8.0;
-    for (int g = 2; g <= 8; g *= 2) {
-      if (pl.tiles_m % g != 0 || pl.tiles_n % (8 / g) != 0) continue;
-      const double rows = (double)M / g + (double)N / (8 / g);
-      if (forced_g == g || (forced_g == 0 && rows < best_rows * 0.999)) {
-        best_rows = rows;
-        pl.xcd_gm = g;
+  // Tile enumeration bands (tile_of): each XCD takes a contiguous range of
+  // about per = tiles/8 tiles, which with bands of g m-tiles covers g m-tiles
+  // x ceil(per/g) n-tiles; its L2 fetches those A rows (bm each) and W rows
+  // (bn each, both halves of a SiLU tile).  The cheapest g wins, the whole
+  // n-column order (g = tiles_m) on ties.  QA_GROUP_M forces g.
+  {
+    const qa::TileShape ts = qa::tile_shape(pl.tile);
+    const int64_t tm = pl.tiles_m, tn = pl.tiles_n;
+    const int64_t per = std::max<int64_t>(1, (tm * tn + 7) / 8);
+    pl.group_m = (int)tm;
+    double best = 1e300;
+    for (int64_t g = tm; g >= 1; g = g > 1 ? (g + 1) / 2 : 0) {
+      // a range longer than a band spans whole bands: ceil(per / tn) m-tiles
+      const int64_t rows = per > g * tn ? (per + tn - 1) / tn : std::min(g, per);
+      const int64_t cols = std::min((per + g - 1) / g, tn);
+      const double cost = (double)rows * ts.bm + (double)cols * ts.bn;
+      if (cost < best * 0.999) {
+        best = cost;
+        pl.group_m = (int)g;
       }
     }
-    if (forced_g == 1) pl.xcd_gm = 1;
+    if (const char* e = getenv("QA_GROUP_M")) {
+      const int g = atoi(e);
+      if (g >= 1) pl.group_m = (int)std::min<int64_t>(g, tm);
+    }
   }
   return pl;
 }
@@ -376,7 +384,7 @@ int qa_linear(qa_ctx* ctx, const qa_linear_desc* d) {
   p.kchunk = plan.kchunk;
   p.accumulate = (d->flags & QA_ACCUMULATE) ? 1 : 0;
   p.bias_rows = (d->flags & QA_BIAS_ROWS) ? 1 : 0;
-  p.xcd_gm = plan.xcd_gm;
+  p.group_m = plan.group_m;
   const int batch = d->batch > 0 ? (int)d->batch : 1;
   if (plan.splits > 1 && batch > 1)
     return fail(QA_EUNSUPPORTED, "qa_linear: split-K with batch > 1");

@@ -28,8 +28,8 @@
 //    answers with zeros: ragged edges cost nothing and need no padding.
 //  * XCD-aware block order: the hardware deals workgroups round-robin over
 //    the 8 XCDs; units are renumbered so each XCD gets a contiguous range of
-//    whole n-blocks of W, or (tile_of, xcd_gm > 1) a rectangle of the tile
-//    grid, whichever makes its L2 fetch fewer operand rows.
+//    a banded tile enumeration (tile_of), sized so its L2 fetches the fewest
+//    A and W rows.
 //  * Split-K: each split writes f32 partials; splitk_reduce_kernel sums them
 //    in split order (deterministic) and runs the epilogue.
 //
@@ -107,31 +107,26 @@ __device__ __forceinline__ int xcd_remap(int b, int n) {
 }
 
 // Block -> (tile m, tile n, k split).  Workgroups are dealt round-robin over
-// the 8 XCDs (block b runs on XCD b % 8), each with its own L2.  With
-// xcd_gm = g > 1 the tile grid is cut into a g x (8/g) grid of rectangles,
-// one per XCD, so an XCD's L2 holds M/g rows of A and N/(8/g) rows of W
-// instead of all of A; otherwise each XCD takes a contiguous range of whole
-// n-blocks (all of A, 1/8 of W).  The planner sets g only when it divides the
-// tile grid.  Within a rectangle, m runs fastest and the k splits of a tile
-// are adjacent.
+// the 8 XCDs (block b runs on XCD b % 8), each with its own L2; xcd_remap
+// gives each XCD a contiguous range of the tile enumeration below, so what an
+// XCD's L2 must fetch is the A rows and W rows one such range touches.  Tiles
+// are enumerated in bands of group_m m-tiles (the last band may be shorter):
+// within a band, m runs fastest, then n, so a range of r tiles covers about
+// group_m m-tiles x r/group_m n-tiles.  group_m = tiles_m enumerates whole
+// n-columns (all of A per XCD), group_m = 1 whole m-rows (all of W); the
+// planner picks the value that fetches the fewest operand rows.  The k splits
+// of a tile are adjacent.
 __device__ __forceinline__ void tile_of(const GemmParams& p, int b, int& tm, int& tn,
                                         int& split) {
-  constexpr int X = 8;
-  const int g = p.xcd_gm;
-  if (g > 1) {
-    const int rm = p.tiles_m / g, rn = p.tiles_n / (X / g);
-    const int xcd = b % X, l = b / X;
-    const int t = l / p.splits;
-    split = l % p.splits;
-    tm = (xcd % g) * rm + t % rm;
-    tn = (xcd / g) * rn + t / rm;
-    return;
-  }
   const int u = xcd_remap(b, p.tiles_m * p.tiles_n * p.splits);
   split = u % p.splits;
   const int t = u / p.splits;
-  tn = t / p.tiles_m;
-  tm = t % p.tiles_m;
+  const int g = p.group_m;
+  const int band = t / (g * p.tiles_n);
+  const int i = t - band * g * p.tiles_n;
+  const int rows = min(g, p.tiles_m - band * g);
+  tm = band * g + i % rows;
+  tn = i / rows;
 }
 
 // s_waitcnt vmcnt(N) leaving expcnt / lgkmcnt unconstrained (gfx9 encoding).
@@ -338,17 +333,24 @@ __device__ __forceinline__ void finish_tile(const GemmParams& p, f32x16 (&acc)[F
   }
 }
 
-// KG k-groups of 4 waves (256*KG threads).  Every wave issues DMA; group g
-// multiplies slices {g*4/KG .. (g+1)*4/KG - 1} of each 64-deep stage on a
-// 2x2 wave layout, so the LDS read traffic per stage does not grow with KG,
-// while the number of waves streaming L2 -> LDS does (a wave sustains only
-// ~7 B/clk of DMA, so 8 waves per CU are needed to feed the matrix cores).
-// The groups' partial accumulators are summed through LDS at the end, group
-// 0 + group 1 + ..., a fixed order.
-template <int DT, int BM, int BN, int S, int EPI, int KG>
-__global__ void __launch_bounds__(NT * KG) gemm_dma_kernel(const GemmParams p) {
-  constexpr int NTH = NT * KG;
-  constexpr int NW = 4 * KG;       // waves
+// KG k-groups of 4 MMA waves; group g multiplies slices
+// {g*4/KG .. (g+1)*4/KG - 1} of each 64-deep stage on a 2x2 wave layout, so
+// the LDS read traffic per stage does not grow with KG.  The groups' partial
+// accumulators are summed through LDS at the end, group 0 + group 1 + ..., a
+// fixed order.
+//
+// Who streams L2 -> LDS: a wave sustains only ~12 GB/s of DMA however deep
+// its queue, so the CU's fill rate grows with the number of waves issuing it
+// (~58 GB/s with 4, ~100 with 8, ~120 with 16), and waves that also issue
+// MFMAs and fragment reads issue DMA more slowly still.  With PW = 0 the MMA
+// waves issue the DMA themselves; with PW > 0, PW producer waves (after the
+// MMA waves) issue all of it and only take part in the barriers and the
+// epilogue.
+template <int DT, int BM, int BN, int S, int EPI, int KG, int PW>
+__global__ void __launch_bounds__(NT * KG + 64 * PW) gemm_dma_kernel(const GemmParams p) {
+  constexpr int NMW = 4 * KG;                // MMA waves
+  constexpr int NTH = NT * KG + 64 * PW;     // threads
+  constexpr int NW = PW > 0 ? PW : NMW;      // DMA-issuing waves
   constexpr int SPG = 4 / KG;      // 16-deep slices per group per stage
   constexpr int WGM = 2, WGN = 2;  // waves along m and n within a group
   constexpr int WTM = BM / WGM, WTN = BN / WGN;
@@ -368,7 +370,10 @@ __global__ void __launch_bounds__(NT * KG) gemm_dma_kernel(const GemmParams p) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int kg = wave >> 2, w4 = wave & 3;
+  const bool mma_wave = PW == 0 || wave < NMW;
+  const bool dma_wave = PW == 0 || wave >= NMW;
+  const int dwave = PW == 0 ? wave : (wave >= NMW ? wave - NMW : 0);  // index among DMA waves
+  const int kg = mma_wave ? wave >> 2 : KG, w4 = wave & 3;  // producers: no k group
   const int wm = w4 % WGM, wn = w4 / WGM;
   const int fr = lane & 31, fh = lane >> 5;  // fragment row, k-chunk parity
 
@@ -389,21 +394,21 @@ __global__ void __launch_bounds__(NT * KG) gemm_dma_kernel(const GemmParams p) {
   const int nk = (kend - kbeg + BK - 1) / BK;
 
   // Per-lane byte offsets at k = 0 of the row chunk this lane fetches: lane l
-  // of DMA instruction j fills LDS row r = (NW*j + wave)*8 + l/8 at physical
+  // of DMA instruction j fills LDS row r = (NW*j + dwave)*8 + l/8 at physical
   // chunk l%8, so it fetches logical chunk (l%8) ^ swz(r).
   const int lrow = lane >> 3, pchunk = lane & 7;
   uint32_t aoff[AJ], woff[BJ];
   int akc[AJ], wkc[BJ];  // k offset (elements) of the fetched chunk
 #pragma unroll
   for (int j = 0; j < AJ; ++j) {
-    const int r = (j * NW + wave) * 8 + lrow;
+    const int r = (j * NW + dwave) * 8 + lrow;
     const int m = m0 + r;
     akc[j] = (pchunk ^ swz(r)) * 8;
     aoff[j] = m < p.M ? (uint32_t)(((int64_t)m * p.lda + akc[j]) * 2) : OOB;
   }
 #pragma unroll
   for (int j = 0; j < BJ; ++j) {
-    const int r = (j * NW + wave) * 8 + lrow;
+    const int r = (j * NW + dwave) * 8 + lrow;
     const int n = w_row<BN, EPI>(p, tn, r);
     wkc[j] = (pchunk ^ swz(r)) * 8;
     woff[j] = n >= 0 ? (uint32_t)(((int64_t)n * p.ldb + wkc[j]) * 2) : OOB;
@@ -416,7 +421,7 @@ __global__ void __launch_bounds__(NT * KG) gemm_dma_kernel(const GemmParams p) {
     for (int j = 0; j < AJ; ++j) {
       const bool ok = k0 + akc[j] < kend && aoff[j] != OOB;
       const uint32_t off = ok ? aoff[j] + (uint32_t)k0 * 2u : OOB;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (QA_LDS void*)(sb + (j * NW + wave) * 1024),
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (QA_LDS void*)(sb + (j * NW + dwave) * 1024),
                                                16, off, 0, 0, 0);
     }
 #pragma unroll
@@ -424,7 +429,7 @@ __global__ void __launch_bounds__(NT * KG) gemm_dma_kernel(const GemmParams p) {
       const bool ok = k0 + wkc[j] < kend && woff[j] != OOB;
       const uint32_t off = ok ? woff[j] + (uint32_t)k0 * 2u : OOB;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rsw, (QA_LDS void*)(sb + SA + (j * NW + wave) * 1024), 16, off, 0, 0, 0);
+          rsw, (QA_LDS void*)(sb + SA + (j * NW + dwave) * 1024), 16, off, 0, 0, 0);
     }
   };
 
@@ -466,9 +471,15 @@ __global__ void __launch_bounds__(NT * KG) gemm_dma_kernel(const GemmParams p) {
   // its own reads of the stage (all of them issued by then), and after the
   // barrier the first fragments of stage it+1 load while the last slice's
   // MFMAs run, so no wave stalls on LDS right after the barrier.
+  //
+  // With producer waves the roles split but the barrier sequence is the same
+  // (one before stage 0, one per later stage): a producer waits for its own
+  // DMA of stage it+1, meets the MMA waves at the barrier (after which stage
+  // it's buffer is free: every MMA wave waited for its reads of it), and
+  // refills that buffer with stage it+S at once.
   static_assert(SPG % 2 == 0, "fragment slots alternate within a stage");
   const int kk0 = kg * SPG;
-  if (nk > 0) {
+  if (nk > 0 && !mma_wave) {
 #pragma unroll
     for (int s = 0; s < S; ++s)
       if (s < nk) issue(s, s);
@@ -476,6 +487,25 @@ __global__ void __launch_bounds__(NT * KG) gemm_dma_kernel(const GemmParams p) {
       wait_vmcnt<(S - 1) * LPS>();
     else
       wait_vmcnt<0>();
+    exec_barrier();
+    for (int it = 0; it + 1 < nk; ++it) {
+      if (it + S - 1 < nk)
+        wait_vmcnt<(S - 2) * LPS>();
+      else
+        wait_vmcnt<0>();
+      exec_barrier();
+      if (it + S < nk) issue(it + S, it % S);
+    }
+  } else if (nk > 0) {
+    if (dma_wave) {
+#pragma unroll
+      for (int s = 0; s < S; ++s)
+        if (s < nk) issue(s, s);
+      if (S - 1 < nk)
+        wait_vmcnt<(S - 1) * LPS>();
+      else
+        wait_vmcnt<0>();
+    }
     exec_barrier();
     read_frags(0, kk0, 0);
     for (int it = 0; it < nk; ++it) {
@@ -487,17 +517,19 @@ __global__ void __launch_bounds__(NT * KG) gemm_dma_kernel(const GemmParams p) {
       }
       wait_lds();  // unconditional: both paths reach the last MFMAs with ready slots
       if (it + 1 < nk) {
-        if (it + S - 1 < nk)
-          wait_vmcnt<(S - 2) * LPS>();
-        else
-          wait_vmcnt<0>();
+        if (dma_wave) {
+          if (it + S - 1 < nk)
+            wait_vmcnt<(S - 2) * LPS>();
+          else
+            wait_vmcnt<0>();
+        }
         exec_barrier();
         read_frags((it + 1) % S, kk0, 0);
       }
       mma((SPG - 1) & 1);
       // Refill the freed buffer behind this wave's LDS reads and MFMAs (issued
       // ahead of them, the DMA writes measurably delay the fragment reads).
-      if (it + 1 < nk && it + S < nk) {
+      if (dma_wave && it + 1 < nk && it + S < nk) {
         __builtin_amdgcn_sched_barrier(0);
         issue(it + S, buf);
       }
@@ -704,11 +736,11 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(const GemmParams p) 
   epilogue4<DT, EPI>(p, p.c, m, n, v, uu);
 }
 
-template <int DT, int BM, int BN, int S, int EPI, int KG>
+template <int DT, int BM, int BN, int S, int EPI, int KG, int PW>
 hipError_t launch_dma(const Plan& plan, const GemmParams& p, int batch, hipStream_t s) {
   const unsigned units = (unsigned)(plan.tiles_m * plan.tiles_n * plan.splits);
-  hipLaunchKernelGGL((gemm_dma_kernel<DT, BM, BN, S, EPI, KG>), dim3(units, (unsigned)batch),
-                     dim3(NT * KG), 0, s, p);
+  hipLaunchKernelGGL((gemm_dma_kernel<DT, BM, BN, S, EPI, KG, PW>), dim3(units, (unsigned)batch),
+                     dim3(NT * KG + 64 * PW), 0, s, p);
   return hipGetLastError();
 }
 
@@ -736,12 +768,12 @@ hipError_t launch_epi(const Plan& plan, const GemmParams& p, int batch, hipStrea
     else e = launch_reg<DT, EPI>(plan, p, batch, s);
   } else {
     switch (plan.tile) {
-      case TILE_256x128: e = launch_dma<DT, 256, 128, 3, EPI, 2>(plan, p, batch, s); break;
-      case TILE_128x256: e = launch_dma<DT, 128, 256, 3, EPI, 2>(plan, p, batch, s); break;
-      case TILE_64x128: e = launch_dma<DT, 64, 128, 4, EPI, 2>(plan, p, batch, s); break;
-      case TILE_64x64: e = launch_dma<DT, 64, 64, 4, EPI, 2>(plan, p, batch, s); break;
-      case TILE_128x192: e = launch_dma<DT, 128, 192, 4, EPI, 2>(plan, p, batch, s); break;
-      default: e = launch_dma<DT, 128, 128, 5, EPI, 2>(plan, p, batch, s); break;
+      case TILE_256x128: e = launch_dma<DT, 256, 128, 3, EPI, 2, 0>(plan, p, batch, s); break;
+      case TILE_128x256: e = launch_dma<DT, 128, 256, 3, EPI, 2, 0>(plan, p, batch, s); break;
+      case TILE_64x128: e = launch_dma<DT, 64, 128, 4, EPI, 2, 8>(plan, p, batch, s); break;
+      case TILE_64x64: e = launch_dma<DT, 64, 64, 4, EPI, 2, 8>(plan, p, batch, s); break;
+      case TILE_128x192: e = launch_dma<DT, 128, 192, 4, EPI, 2, 0>(plan, p, batch, s); break;
+      default: e = launch_dma<DT, 128, 128, 5, EPI, 2, 8>(plan, p, batch, s); break;
     }
   }
   if (e != hipSuccess || plan.splits == 1) return e;

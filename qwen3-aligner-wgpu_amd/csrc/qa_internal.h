@@ -56,7 +56,7 @@ struct GemmParams {
   int kchunk;            // K range per split, multiple of 64
   int accumulate;        // add C_old before the rounding
   int bias_rows;         // bias indexed by output row (channel-major conv)
-  int xcd_gm;            // XCD rectangles along m (1 = whole n-blocks per XCD)
+  int group_m;           // m-tiles per band of the tile enumeration (tile_of)
 };
 
 struct Plan {
@@ -64,7 +64,7 @@ struct Plan {
   int epi;
   bool transb;
   int tiles_m, tiles_n, splits, kchunk;
-  int xcd_gm;         // see GemmParams::xcd_gm
+  int group_m;        // see GemmParams::group_m
   size_t ws_floats;   // split-K partial floats needed
 };
 

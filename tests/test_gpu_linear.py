@@ -180,29 +180,30 @@ def test_forced_tiles_and_splits(ctx, pkg, orc, tile, splits):
     assert_silu_mul(act, act_exact, a, gu_w, gu_exact, orc, 0, k)
 
 
-@pytest.mark.parametrize("xcd_gm", [1, 2, 4, 8])
+@pytest.mark.parametrize("group_m", [1, 3, 5, 8, 1000])
 @pytest.mark.parametrize("tile,splits", [(4, 1), (0, 1), (3, 2), (5, 1)])
-def test_xcd_tile_grids(ctx, pkg, orc, xcd_gm, tile, splits):
-    """Every XCD rectangle grid maps blocks onto tiles one to one: C starts as
-    noise and must end equal to the exactly rounded result everywhere (a tile
-    computed twice leaves another one untouched)."""
-    rng = np.random.default_rng(40 + xcd_gm + 10 * tile)
-    m, n, k = 512, 1536, 640   # 64x64: 8x24 tiles; 128x128: 4x12; 64x128: 8x12; 128x192: 4x8
+def test_tile_enumeration_bands(ctx, pkg, orc, group_m, tile, splits):
+    """Every band height of the tile enumeration (including ones that do not
+    divide the tile grid, and more than its height) maps blocks onto tiles
+    one to one: C starts as noise and must end equal to the exactly rounded
+    result everywhere (a tile computed twice leaves another one untouched)."""
+    rng = np.random.default_rng(40 + group_m + 10 * tile)
+    m, n, k = 600, 1472, 640   # ragged in m and n for every tile shape
     a, w = _case(rng, orc, 0, m, n, k)
     c0 = _h16(orc, rng.standard_normal((m, n)), 0)
-    os.environ.update(QA_TILE=str(tile), QA_SPLITS=str(splits), QA_XCD_GM=str(xcd_gm))
+    os.environ.update(QA_TILE=str(tile), QA_SPLITS=str(splits), QA_GROUP_M=str(group_m))
     try:
         got = _run(ctx, pkg, 0, a, w, c0)
-        gu_w = _h16(orc, 0.05 * rng.standard_normal((2 * 768, k)), 0)
-        act = _run(ctx, pkg, 0, a, gu_w, np.zeros((m, 768), np.uint16), flags=pkg.EPI_SILU_MUL)
+        gu_w = _h16(orc, 0.05 * rng.standard_normal((2 * 736, k)), 0)
+        act = _run(ctx, pkg, 0, a, gu_w, np.zeros((m, 736), np.uint16), flags=pkg.EPI_SILU_MUL)
     finally:
-        for key in ("QA_TILE", "QA_SPLITS", "QA_XCD_GM"):
+        for key in ("QA_TILE", "QA_SPLITS", "QA_GROUP_M"):
             del os.environ[key]
     exact = orc.linear(0, a, w, np.zeros_like(c0), flags=orc.EXACT)
     assert_parity(got, exact, orc, 0, ulp_tol=1)
-    act_exact = orc.linear(0, a, gu_w, np.zeros((m, 768), np.uint16),
+    act_exact = orc.linear(0, a, gu_w, np.zeros((m, 736), np.uint16),
                            flags=orc.EPI_SILU_MUL | orc.EXACT)
-    gu_exact = orc.linear(0, a, gu_w, np.zeros((m, 1536), np.uint16), flags=orc.EXACT)
+    gu_exact = orc.linear(0, a, gu_w, np.zeros((m, 1472), np.uint16), flags=orc.EXACT)
     assert_silu_mul(act, act_exact, a, gu_w, gu_exact, orc, 0, k)
 
 
