@@ -771,7 +771,7 @@ hipError_t launch_epi(const Plan& plan, const GemmParams& p, int batch, hipStrea
       case TILE_256x128: e = launch_dma<DT, 256, 128, 3, EPI, 2, 0>(plan, p, batch, s); break;
       case TILE_128x256: e = launch_dma<DT, 128, 256, 3, EPI, 2, 0>(plan, p, batch, s); break;
       case TILE_64x128: e = launch_dma<DT, 64, 128, 4, EPI, 2, 8>(plan, p, batch, s); break;
-      case TILE_64x64: e = launch_dma<DT, 64, 64, 4, EPI, 2, 8>(plan, p, batch, s); break;
+      case TILE_64x64: e = launch_dma<DT, 64, 64, 6, EPI, 2, 8>(plan, p, batch, s); break;
       case TILE_128x192: e = launch_dma<DT, 128, 192, 4, EPI, 2, 0>(plan, p, batch, s); break;
       default: e = launch_dma<DT, 128, 128, 5, EPI, 2, 8>(plan, p, batch, s); break;
     }
