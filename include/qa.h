@@ -138,7 +138,8 @@ int qa_ctx_destroy(qa_ctx* ctx);
  * `gpu.queue`). */
 void* qa_ctx_stream(qa_ctx* ctx);
 
-/* Device memory (Gpu::storage, src/gpu.rs:672-682: sizes padded to 16 B). */
+/* Device memory (Gpu::storage, src/gpu.rs:672-682: sizes padded to 16 B,
+ * contents zero-filled as wgpu's are). */
 int qa_alloc(qa_ctx* ctx, size_t bytes, void** out);
 int qa_free(qa_ctx* ctx, void* ptr);
 /* Host -> device copy at byte offset `off`; the host bytes are consumed
@@ -157,6 +158,93 @@ int qa_linear(qa_ctx* ctx, const qa_linear_desc* desc);
 int qa_linear_validate(const qa_linear_desc* desc);
 /* Launch the MLP block (see qa_mlp_desc). */
 int qa_mlp_fused(qa_ctx* ctx, const qa_mlp_desc* desc);
+
+/* ---- decoder prefill ops around the projections ----------------------- */
+
+/* y[r] = round(x[r] * inv_r * w), inv_r = 1 / sqrt(mean(x[r]^2) + eps) in
+ * f32: the input and post-attention norms.  Replaces the `rms_norm` pipeline
+ * dispatch (src/decoder.rs:1305-1319,1610-1626; WGSL src/shaders.rs:331-383;
+ * CPU twin `rms_norm_row`, src/cpu_decoder.rs:288-300).  n and the row
+ * strides are multiples of 8; x, y 16-byte aligned. */
+typedef struct qa_rms_norm_desc {
+  uint32_t dtype;
+  uint32_t flags; /* reserved, must be 0 */
+  int64_t rows, n;
+  const void* x;
+  int64_t ldx;
+  const float* w; /* [n], the norm weight widened to f32 */
+  void* y;
+  int64_t ldy;
+  float eps;
+} qa_rms_norm_desc;
+int qa_rms_norm(qa_ctx* ctx, const qa_rms_norm_desc* desc);
+
+/* Per-head q / k RMSNorm + rotate-half RoPE and the KV-cache write, for
+ * `rows` positions pos0.. of the fused qkv GEMM output: replaces the
+ * `qkv_extract` dispatch (src/decoder.rs:1330-1344; WGSL
+ * src/shaders.rs:910-1031; CPU twin src/cpu_decoder.rs:302-322,464-491).
+ *   qkv     [rows][(nqh + 2 nkvh) hd], row stride ldqkv: q heads, k, v
+ *   cos,sin [pos][hd] f32 tables (src/mrope.rs:55-82); row pos0 + r is used
+ *   q_out   [nqh][rows][hd]   q heads, normed + roped (head-major)
+ *   k_cache [nkvh][cap][hd]   k heads, normed + roped, at rows start..
+ *   v_cache [nkvh][hd][cap]   v heads verbatim, TRANSPOSED: key t at column
+ *                             t with bits 2 and 3 swapped (each aligned group
+ *                             of 16 keys stored 0-3, 8-11, 4-7, 12-15)
+ * The V cache is kept transposed (and so ordered) so that qa_attention_prefill's
+ * P.V matrix product reads each fragment's keys as one 16-byte run.  hd is a
+ * multiple of 64 (<= 256); cap is a multiple of 16; start + rows <= cap. */
+typedef struct qa_qk_rope_desc {
+  uint32_t dtype;
+  uint32_t flags; /* reserved, must be 0 */
+  int64_t rows;
+  int32_t nqh, nkvh, hd;
+  float eps;
+  const void* qkv;
+  int64_t ldqkv;
+  const float* qn_w; /* [hd] */
+  const float* kn_w; /* [hd] */
+  const float* cos;
+  const float* sin;
+  int64_t pos0;
+  void* q_out;
+  void* k_cache;
+  void* v_cache;
+  int64_t cap, start;
+} qa_qk_rope_desc;
+int qa_qk_norm_rope(qa_ctx* ctx, const qa_qk_rope_desc* desc);
+
+/* Causal GQA attention for `rows` query positions q0.. (q head h reads kv
+ * head h / (nqh / nkvh); row r attends to cache rows 0..q0 + r), softmax of
+ * q.k / sqrt(hd) in f32, out[r][h hd + j] = round(sum_t p_t v_t[j]).  Replaces
+ * the prefill attention chain repeat_kv -> scores -> softmax -> P.V (-> slab
+ * merge) (src/decoder.rs:1346-1600; WGSL src/shaders.rs:2079-2505; CPU twin
+ * `attention`, src/cpu_decoder.rs:324-411).  q, k_cache and v_cache are laid
+ * out as qa_qk_norm_rope writes them; out is [rows][nqh hd] with row stride
+ * ldo, the o projection's input.  hd = 128, nqh / nkvh in {1, 2}; cap is a
+ * multiple of 16; q0 + rows <= cap.  Cache entries from q0 + rows up to the
+ * next multiple of 64 keys are read (and weighted by zero): they must hold
+ * finite values, as qa_alloc's zero-filled memory does.
+ * By default the probabilities enter the P.V product as two 16-bit terms
+ * (value + rounding residue), so the result tracks the f32 CPU twin; with
+ * QA_ATTN_P16 they are rounded once to the 16-bit format, as the reference's
+ * GPU path rounds them (its softmax writes 16-bit P for the P.V GEMM,
+ * src/shaders.rs:2226-2294; it also rounds the scores, which this kernel keeps
+ * in f32) -- faster, up to 2^-11 (f16) / 2^-8 (bf16) relative error per
+ * weight. */
+enum { QA_ATTN_P16 = 1u << 0 };
+typedef struct qa_attention_desc {
+  uint32_t dtype;
+  uint32_t flags; /* 0 or QA_ATTN_P16 */
+  int64_t rows;
+  int32_t nqh, nkvh, hd;
+  const void* q;
+  const void* k_cache;
+  const void* v_cache;
+  int64_t cap, q0;
+  void* out;
+  int64_t ldo;
+} qa_attention_desc;
+int qa_attention_prefill(qa_ctx* ctx, const qa_attention_desc* desc);
 
 /* Message of the last failure on this thread ("" if none). */
 const char* qa_last_error(void);

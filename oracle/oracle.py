@@ -81,6 +81,16 @@ def lib() -> ctypes.CDLL:
         L.or_gelu.argtypes = [ctypes.c_float]
         L.or_linear.restype = ctypes.c_int
         L.or_linear.argtypes = [ctypes.POINTER(LinearDesc)]
+        ci, f = ctypes.c_int, ctypes.c_float
+        L.or_rms_norm.argtypes = [ci, i64, i64, p, i64, p, f, p, i64]
+        L.or_rms_norm.restype = None
+        L.or_qk_norm_rope.argtypes = [ci, i64, ci, ci, ci, p, i64, p, p, p, p, i64, f, p, p, p,
+                                      i64, i64]
+        L.or_qk_norm_rope.restype = None
+        L.or_attention.argtypes = [ci, i64, ci, ci, ci, p, p, p, i64, i64, p, i64]
+        L.or_attention.restype = None
+        L.or_vperm.argtypes = [i64]
+        L.or_vperm.restype = i64
         L.or_num_threads.restype = ctypes.c_int
         _lib = L
     return _lib
@@ -189,3 +199,52 @@ def linear(dtype: int, a: np.ndarray, w: np.ndarray, c: np.ndarray, *, flags: in
 
 def num_threads() -> int:
     return lib().or_num_threads()
+
+
+def rms_norm(dtype: int, x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    """or_rms_norm: x [rows, n] 16-bit bits, w [n] f32 -> [rows, n] bits."""
+    x = _c(x, np.uint16)
+    w = _c(w, np.float32)
+    rows, n = x.shape
+    y = np.empty_like(x)
+    lib().or_rms_norm(dtype, rows, n, _ptr(x), n, _ptr(w), ctypes.c_float(eps), _ptr(y), n)
+    return y
+
+
+def qk_norm_rope(dtype: int, qkv: np.ndarray, nqh: int, nkvh: int, hd: int, qn: np.ndarray,
+                 kn: np.ndarray, cos_t: np.ndarray, sin_t: np.ndarray, pos0: int, eps: float,
+                 k_cache: np.ndarray, v_cache: np.ndarray, start: int) -> np.ndarray:
+    """or_qk_norm_rope: returns q_out [nqh, rows, hd]; writes k_cache [nkvh, cap, hd]
+    and the transposed v_cache [nkvh, hd, cap] in place."""
+    qkv = _c(qkv, np.uint16)
+    rows = qkv.shape[0]
+    cap = k_cache.shape[1]
+    for arr in (k_cache, v_cache):
+        assert arr.dtype == np.uint16 and arr.flags.c_contiguous
+    q_out = np.empty((nqh, rows, hd), np.uint16)
+    lib().or_qk_norm_rope(dtype, rows, nqh, nkvh, hd, _ptr(qkv), qkv.shape[1],
+                          _ptr(_c(qn, np.float32)), _ptr(_c(kn, np.float32)),
+                          _ptr(_c(cos_t, np.float32)), _ptr(_c(sin_t, np.float32)), pos0,
+                          ctypes.c_float(eps), _ptr(q_out), _ptr(k_cache), _ptr(v_cache), cap,
+                          start)
+    return q_out
+
+
+def vperm(n: int) -> np.ndarray:
+    """or_vperm over 0..n-1: the V-cache column of each key."""
+    return np.array([lib().or_vperm(t) for t in range(n)], np.int64)
+
+
+def attention(dtype: int, q: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray,
+              q0: int) -> np.ndarray:
+    """or_attention: q [nqh, rows, hd], k_cache [nkvh, cap, hd], v_cache [nkvh, hd, cap]
+    -> out [rows, nqh * hd]."""
+    q = _c(q, np.uint16)
+    k_cache = _c(k_cache, np.uint16)
+    v_cache = _c(v_cache, np.uint16)
+    nqh, rows, hd = q.shape
+    nkvh, cap, _ = k_cache.shape
+    out = np.empty((rows, nqh * hd), np.uint16)
+    lib().or_attention(dtype, rows, nqh, nkvh, hd, _ptr(q), _ptr(k_cache), _ptr(v_cache), cap,
+                       q0, _ptr(out), nqh * hd)
+    return out

@@ -95,6 +95,23 @@ int or_linear(const or_linear_desc* d);
 /* Number of OpenMP threads the oracle's parallel loops use. */
 int or_num_threads(void);
 
+/* ---- decoder prefill ops around the projections (qa_oracle_decoder.c) ----
+ * Parity pins (tests/test_oracle_decoder.py): f64 closed forms of RMSNorm and
+ * of norm + rotate-half RoPE (including pos 0 = plain norm and the pairwise
+ * rotation invariant), brute-force f64 softmax attention, the causal
+ * invariant (a row ignores later keys), uniform scores averaging V, and GQA
+ * head sharing. */
+int64_t or_vperm(int64_t t); /* V-cache column of key t (bits 2 and 3 swapped) */
+void or_rms_norm(int dtype, int64_t rows, int64_t n, const uint16_t* x, int64_t ldx,
+                 const float* w, float eps, uint16_t* y, int64_t ldy);
+void or_qk_norm_rope(int dtype, int64_t rows, int nqh, int nkvh, int hd, const uint16_t* qkv,
+                     int64_t ldqkv, const float* qn, const float* kn, const float* cos_t,
+                     const float* sin_t, int64_t pos0, float eps, uint16_t* q_out,
+                     uint16_t* k_cache, uint16_t* v_cache, int64_t cap, int64_t start);
+void or_attention(int dtype, int64_t rows, int nqh, int nkvh, int hd, const uint16_t* q,
+                  const uint16_t* k_cache, const uint16_t* v_cache, int64_t cap, int64_t q0,
+                  uint16_t* out, int64_t ldo);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,4 +1,5 @@
-"""MI355X-native linear-layer GEMM path of qwen3-aligner-wgpu.
+"""MI355X-native linear-layer GEMM path of qwen3-aligner-wgpu (and the decoder
+prefill ops around it).
 
 Python binding (ctypes) of the C ABI in include/qa.h, implemented by
 csrc/libqa.so (hand-written gfx950 MFMA kernels), and of the C++ host mirror of
@@ -27,6 +28,7 @@ INCLUDE_DIR = os.path.join(os.path.dirname(_HERE), "include")
 QA_OK, QA_EINVAL, QA_ENOMEM, QA_EDEVICE, QA_EUNSUPPORTED = 0, -1, -2, -3, -4
 F16, BF16 = 0, 1
 ACCUMULATE, EPI_GELU, EPI_SILU_MUL, TRANSB, BIAS_ROWS = 1, 2, 4, 8, 16
+QA_ATTN_P16 = 1  # qa_attention_desc.flags
 
 _STATUS = {
     QA_EINVAL: "QA_EINVAL",
@@ -85,11 +87,75 @@ class MlpDesc(ctypes.Structure):
     ]
 
 
+class RmsNormDesc(ctypes.Structure):
+    """qa_rms_norm_desc (include/qa.h)."""
+
+    _fields_ = [
+        ("dtype", ctypes.c_uint32),
+        ("flags", ctypes.c_uint32),
+        ("rows", ctypes.c_int64),
+        ("n", ctypes.c_int64),
+        ("x", ctypes.c_void_p),
+        ("ldx", ctypes.c_int64),
+        ("w", ctypes.c_void_p),
+        ("y", ctypes.c_void_p),
+        ("ldy", ctypes.c_int64),
+        ("eps", ctypes.c_float),
+    ]
+
+
+class QkRopeDesc(ctypes.Structure):
+    """qa_qk_rope_desc (include/qa.h)."""
+
+    _fields_ = [
+        ("dtype", ctypes.c_uint32),
+        ("flags", ctypes.c_uint32),
+        ("rows", ctypes.c_int64),
+        ("nqh", ctypes.c_int32),
+        ("nkvh", ctypes.c_int32),
+        ("hd", ctypes.c_int32),
+        ("eps", ctypes.c_float),
+        ("qkv", ctypes.c_void_p),
+        ("ldqkv", ctypes.c_int64),
+        ("qn_w", ctypes.c_void_p),
+        ("kn_w", ctypes.c_void_p),
+        ("cos", ctypes.c_void_p),
+        ("sin", ctypes.c_void_p),
+        ("pos0", ctypes.c_int64),
+        ("q_out", ctypes.c_void_p),
+        ("k_cache", ctypes.c_void_p),
+        ("v_cache", ctypes.c_void_p),
+        ("cap", ctypes.c_int64),
+        ("start", ctypes.c_int64),
+    ]
+
+
+class AttentionDesc(ctypes.Structure):
+    """qa_attention_desc (include/qa.h)."""
+
+    _fields_ = [
+        ("dtype", ctypes.c_uint32),
+        ("flags", ctypes.c_uint32),
+        ("rows", ctypes.c_int64),
+        ("nqh", ctypes.c_int32),
+        ("nkvh", ctypes.c_int32),
+        ("hd", ctypes.c_int32),
+        ("q", ctypes.c_void_p),
+        ("k_cache", ctypes.c_void_p),
+        ("v_cache", ctypes.c_void_p),
+        ("cap", ctypes.c_int64),
+        ("q0", ctypes.c_int64),
+        ("out", ctypes.c_void_p),
+        ("ldo", ctypes.c_int64),
+    ]
+
+
 # Every symbol include/qa.h declares (checked by tests/test_abi.py).
 EXPORTS = (
     "qa_ctx_create", "qa_ctx_destroy", "qa_ctx_stream", "qa_alloc", "qa_free",
     "qa_upload", "qa_download", "qa_sync", "qa_linear", "qa_linear_validate",
-    "qa_mlp_fused", "qa_last_error", "qa_version",
+    "qa_mlp_fused", "qa_rms_norm", "qa_qk_norm_rope", "qa_attention_prefill",
+    "qa_last_error", "qa_version",
 )
 
 _lib = None
@@ -116,6 +182,9 @@ def lib() -> ctypes.CDLL:
         L.qa_linear.argtypes = [vp, ctypes.POINTER(LinearDesc)]
         L.qa_linear_validate.argtypes = [ctypes.POINTER(LinearDesc)]
         L.qa_mlp_fused.argtypes = [vp, ctypes.POINTER(MlpDesc)]
+        L.qa_rms_norm.argtypes = [vp, ctypes.POINTER(RmsNormDesc)]
+        L.qa_qk_norm_rope.argtypes = [vp, ctypes.POINTER(QkRopeDesc)]
+        L.qa_attention_prefill.argtypes = [vp, ctypes.POINTER(AttentionDesc)]
         L.qa_last_error.restype = ctypes.c_char_p
         L.qa_version.restype = ctypes.c_char_p
         for name in EXPORTS:
@@ -217,6 +286,15 @@ class Context:
 
     def mlp_fused(self, desc: MlpDesc) -> None:
         check(lib().qa_mlp_fused(self.handle, ctypes.byref(desc)))
+
+    def rms_norm(self, desc: RmsNormDesc) -> None:
+        check(lib().qa_rms_norm(self.handle, ctypes.byref(desc)))
+
+    def qk_norm_rope(self, desc: QkRopeDesc) -> None:
+        check(lib().qa_qk_norm_rope(self.handle, ctypes.byref(desc)))
+
+    def attention_prefill(self, desc: AttentionDesc) -> None:
+        check(lib().qa_attention_prefill(self.handle, ctypes.byref(desc)))
 
 
 def linear_desc(dtype: int, m: int, n: int, k: int, a, w, c, *, flags: int = 0, bias=None,

@@ -307,8 +307,16 @@ int qa_alloc(qa_ctx* ctx, size_t bytes, void** out) {
   if (int rc = set_device(ctx)) return rc;
   const size_t padded = std::max<size_t>(16, (bytes + 15) & ~(size_t)15);
   void* p = nullptr;
-  const hipError_t e = hipMalloc(&p, padded);
+  hipError_t e = hipMalloc(&p, padded);
   if (e != hipSuccess) return hip_fail(e, "hipMalloc");
+  // Zero-filled, as wgpu storage buffers are (the attention reads cache
+  // entries past the written rows with weight zero; they must be finite).
+  e = hipMemsetAsync(p, 0, padded, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) {
+    (void)hipFree(p);
+    return hip_fail(e, "hipMemsetAsync(qa_alloc)");
+  }
   *out = p;
   return ok();
 }
@@ -427,6 +435,124 @@ int qa_mlp_fused(qa_ctx* ctx, const qa_mlp_desc* d) {
   if (int rc = validate(&down)) return rc;
   if (int rc = qa_linear(ctx, &gu)) return rc;
   return qa_linear(ctx, &down);
+}
+
+int qa_rms_norm(qa_ctx* ctx, const qa_rms_norm_desc* d) {
+  if (!ctx || !d) return fail(QA_EINVAL, "qa_rms_norm: null argument");
+  if (d->dtype != QA_F16 && d->dtype != QA_BF16)
+    return fail(QA_EINVAL, "qa_rms_norm: dtype %u is neither QA_F16 nor QA_BF16", d->dtype);
+  if (d->flags) return fail(QA_EINVAL, "qa_rms_norm: flags must be 0");
+  if (d->rows < 0 || d->n <= 0 || d->n % 8 || d->n > kI32)
+    return fail(QA_EINVAL, "qa_rms_norm: rows >= 0 and n a positive multiple of 8, got %lld x %lld",
+                (long long)d->rows, (long long)d->n);
+  if (d->ldx < d->n || d->ldy < d->n || d->ldx % 8 || d->ldy % 8)
+    return fail(QA_EINVAL, "qa_rms_norm: row strides must be >= n and multiples of 8");
+  if (!d->x || !d->y || !d->w) return fail(QA_EINVAL, "qa_rms_norm: null pointer");
+  if (!aligned(d->x, 16) || !aligned(d->y, 16) || !aligned(d->w, 4))
+    return fail(QA_EINVAL, "qa_rms_norm: x and y must be 16-byte aligned");
+  if (!(d->eps >= 0.0f)) return fail(QA_EINVAL, "qa_rms_norm: eps must be >= 0");
+  if (d->rows == 0) return ok();
+  if (int rc = set_device(ctx)) return rc;
+  qa::RmsParams p{};
+  p.x = (const uint16_t*)d->x;
+  p.w = d->w;
+  p.y = (uint16_t*)d->y;
+  p.rows = d->rows;
+  p.ldx = d->ldx;
+  p.ldy = d->ldy;
+  p.n = (int)d->n;
+  p.eps = d->eps;
+  const hipError_t e = qa::launch_rms_norm((int)d->dtype, p, ctx->stream);
+  return e == hipSuccess ? ok() : hip_fail(e, "qa_rms_norm launch");
+}
+
+int qa_qk_norm_rope(qa_ctx* ctx, const qa_qk_rope_desc* d) {
+  if (!ctx || !d) return fail(QA_EINVAL, "qa_qk_norm_rope: null argument");
+  if (d->dtype != QA_F16 && d->dtype != QA_BF16)
+    return fail(QA_EINVAL, "qa_qk_norm_rope: dtype %u is neither QA_F16 nor QA_BF16", d->dtype);
+  if (d->flags) return fail(QA_EINVAL, "qa_qk_norm_rope: flags must be 0");
+  if (d->rows < 0 || d->nqh <= 0 || d->nkvh <= 0 || d->nqh % d->nkvh)
+    return fail(QA_EINVAL, "qa_qk_norm_rope: need rows >= 0 and nqh a multiple of nkvh > 0");
+  if (d->hd <= 0 || d->hd % 64 || d->hd > 256)
+    return fail(QA_EINVAL, "qa_qk_norm_rope: hd=%d must be a multiple of 64 up to 256", d->hd);
+  if (d->ldqkv < (int64_t)(d->nqh + 2 * d->nkvh) * d->hd)
+    return fail(QA_EINVAL, "qa_qk_norm_rope: ldqkv below the fused q|k|v width");
+  if (d->pos0 < 0 || d->start < 0 || d->start + d->rows > d->cap || d->cap % 16 || d->cap > kI32)
+    return fail(QA_EINVAL,
+                "qa_qk_norm_rope: need pos0, start >= 0, start + rows <= cap, cap a multiple of 16");
+  if (!d->qkv || !d->qn_w || !d->kn_w || !d->cos || !d->sin || !d->q_out || !d->k_cache ||
+      !d->v_cache)
+    return fail(QA_EINVAL, "qa_qk_norm_rope: null pointer");
+  if (!aligned(d->qkv, 2) || !aligned(d->q_out, 2) || !aligned(d->k_cache, 2) ||
+      !aligned(d->v_cache, 2) || !aligned(d->qn_w, 4) || !aligned(d->kn_w, 4) ||
+      !aligned(d->cos, 4) || !aligned(d->sin, 4))
+    return fail(QA_EINVAL, "qa_qk_norm_rope: misaligned pointer");
+  if (!(d->eps >= 0.0f)) return fail(QA_EINVAL, "qa_qk_norm_rope: eps must be >= 0");
+  if (d->rows == 0) return ok();
+  if (int rc = set_device(ctx)) return rc;
+  qa::RopeParams p{};
+  p.qkv = (const uint16_t*)d->qkv;
+  p.qn = d->qn_w;
+  p.kn = d->kn_w;
+  p.cos = d->cos;
+  p.sin = d->sin;
+  p.q_out = (uint16_t*)d->q_out;
+  p.k_cache = (uint16_t*)d->k_cache;
+  p.v_cache = (uint16_t*)d->v_cache;
+  p.rows = d->rows;
+  p.ldqkv = d->ldqkv;
+  p.pos0 = d->pos0;
+  p.cap = d->cap;
+  p.start = d->start;
+  p.nqh = d->nqh;
+  p.nkvh = d->nkvh;
+  p.hd = d->hd;
+  p.eps = d->eps;
+  const hipError_t e = qa::launch_qk_norm_rope((int)d->dtype, p, ctx->stream);
+  return e == hipSuccess ? ok() : hip_fail(e, "qa_qk_norm_rope launch");
+}
+
+int qa_attention_prefill(qa_ctx* ctx, const qa_attention_desc* d) {
+  if (!ctx || !d) return fail(QA_EINVAL, "qa_attention_prefill: null argument");
+  if (d->dtype != QA_F16 && d->dtype != QA_BF16)
+    return fail(QA_EINVAL, "qa_attention_prefill: dtype %u is neither QA_F16 nor QA_BF16",
+                d->dtype);
+  if (d->flags & ~QA_ATTN_P16)
+    return fail(QA_EINVAL, "qa_attention_prefill: unknown flags 0x%x", d->flags & ~QA_ATTN_P16);
+  if (d->rows < 0 || d->nqh <= 0 || d->nkvh <= 0 || d->nqh % d->nkvh)
+    return fail(QA_EINVAL, "qa_attention_prefill: need rows >= 0 and nqh a multiple of nkvh > 0");
+  if (d->hd != 128) return fail(QA_EUNSUPPORTED, "qa_attention_prefill: hd=%d (only 128)", d->hd);
+  if (d->q0 < 0 || d->q0 + d->rows > d->cap || d->cap * d->hd * 2 > kI32)
+    return fail(QA_EINVAL,
+                "qa_attention_prefill: need q0 >= 0, q0 + rows <= cap and a cache head below 2 GiB");
+  if (d->cap % 16) return fail(QA_EINVAL, "qa_attention_prefill: cap must be a multiple of 16");
+  if (d->nqh / d->nkvh > 2)
+    return fail(QA_EUNSUPPORTED, "qa_attention_prefill: nqh / nkvh = %d (1 or 2 supported)",
+                d->nqh / d->nkvh);
+  if (d->ldo < (int64_t)d->nqh * d->hd || d->ldo % 8)
+    return fail(QA_EINVAL, "qa_attention_prefill: ldo must be >= nqh*hd and a multiple of 8");
+  if (!d->q || !d->k_cache || !d->v_cache || !d->out)
+    return fail(QA_EINVAL, "qa_attention_prefill: null pointer");
+  if (!aligned(d->q, 16) || !aligned(d->k_cache, 16) || !aligned(d->v_cache, 16) ||
+      !aligned(d->out, 16))
+    return fail(QA_EINVAL, "qa_attention_prefill: buffers must be 16-byte aligned");
+  if (d->rows == 0) return ok();
+  if (int rc = set_device(ctx)) return rc;
+  qa::AttnParams p{};
+  p.q = (const uint16_t*)d->q;
+  p.k_cache = (const uint16_t*)d->k_cache;
+  p.v_cache = (const uint16_t*)d->v_cache;
+  p.out = (uint16_t*)d->out;
+  p.rows = d->rows;
+  p.cap = d->cap;
+  p.q0 = d->q0;
+  p.ldo = d->ldo;
+  p.nqh = d->nqh;
+  p.nkvh = d->nkvh;
+  p.hd = d->hd;
+  p.scale = 1.0f / sqrtf((float)d->hd);
+  const hipError_t e = qa::launch_attention((int)d->dtype, p, (d->flags & QA_ATTN_P16) != 0, ctx->stream);
+  return e == hipSuccess ? ok() : hip_fail(e, "qa_attention_prefill launch");
 }
 
 }  // extern "C"

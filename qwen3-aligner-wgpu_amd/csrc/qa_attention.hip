@@ -1,0 +1,350 @@
+// qa_attention.hip -- causal GQA prefill attention for gfx950 (hd = 128).
+//
+// Replaces the reference's prefill attention chain (src/decoder.rs:1346-1600:
+// repeat_kv, a scores GEMM per key slab, softmax, the P.V GEMM and the slab
+// merge; WGSL src/shaders.rs:2079-2505) with one flash-style kernel; the
+// arithmetic it must match is the CPU twin, src/cpu_decoder.rs:324-411: f32
+// scores q.k / sqrt(hd), softmax in f32, out = round(sum_t p_t v_t).
+//
+// Block = one kv head x a tile of 64 query rows x its REP q heads; waves:
+// NS = 2 key splits x REP heads x 2 row groups of 32.  Split s takes the key
+// blocks kb = s, s + 2, ... (64 keys each) below the tile's causal bound, so
+// the long rows' key range is processed by two wave groups at once; the two
+// partial results merge through LDS at the end in a fixed order.
+//
+// Per key block, per wave (32 query rows):
+//  * S = K . Q^T on v_mfma_f32_32x32x16 (A = 32 keys x 16 d from LDS, B = the
+//    wave's Q fragments, kept in registers for the whole kernel): the lane
+//    holds one query row and 16 of each 32-key tile's scores.
+//  * online softmax in the log2 domain (v_exp_f32): row max / sum over the
+//    lane's values plus its partner lane (lane ^ 32, same row); the running
+//    output is rescaled by exp2(m_old - m_new).
+//  * O^T += V^T . P^T: P goes from the score registers straight into the
+//    MFMA's B operand.  The reference's GPU path rounds its probabilities to
+//    the 16-bit format before its P.V GEMM (PS = 1 here), which costs up to
+//    2^-11 (f16) / 2^-8 (bf16) relative per weight; by default (PS = 2) the
+//    rounding residue goes through a second MFMA as a second 16-bit term, so
+//    the product carries ~2^-22 / 2^-16 and the result tracks the f32 CPU
+//    path.  f16 probabilities are formed scaled by 2^15 so that none of them
+//    is subnormal (the scale cancels in the final division).  A lane half holds
+//    keys {16j+4h..+3, 16j+8+4h..+3} of slice j, so the transposed V cache
+//    stores each aligned group of 16 keys in the order 0-3, 8-11, 4-7, 12-15
+//    (bits 2 and 3 of the key swapped): one 16-byte read per V fragment.
+//  * K and V tiles stream L2 -> LDS with buffer_load ... lds, double-buffered
+//    per split group; chunks are XOR-swizzled per row so the 32-row fragment
+//    reads hit distinct banks.
+#include "qa_internal.h"
+
+namespace qa {
+namespace {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+#define QA_LDS __attribute__((address_space(3)))
+
+constexpr uint32_t OOB = 0x80000000u;
+constexpr int HD = 128;  // head dim
+constexpr int QT = 64;   // query rows per block
+constexpr int KB = 64;   // keys per block
+constexpr int NS = 2;    // key splits per block
+constexpr float kLog2e = 1.44269504088896341f;
+
+template <int DT>
+struct AFmt;
+template <>
+struct AFmt<QA_F16> {
+  __device__ static __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  __device__ static __forceinline__ uint32_t narrow(float v) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v);
+  }
+  __device__ static __forceinline__ float widen(uint32_t h) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+  }
+  // Probabilities are formed as p * 2^15 (<= 32768): the f16 range keeps them
+  // normal down to p = 2^-29, so rounding them loses only relative precision.
+  static constexpr float kPBias = 15.f;
+};
+template <>
+struct AFmt<QA_BF16> {
+  __device__ static __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  __device__ static __forceinline__ uint32_t narrow(float v) {  // src/shaders.rs:169-179
+    const uint32_t u = __float_as_uint(v);
+    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  }
+  __device__ static __forceinline__ float widen(uint32_t h) { return __uint_as_float(h << 16); }
+  static constexpr float kPBias = 0.f;
+};
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+__device__ __forceinline__ void wait_lds() {
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_waitcnt(0xF | (0x3 << 14) | (0x7 << 4) | (0x0 << 8));
+}
+__device__ __forceinline__ void exec_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// LDS tile layouts.  K tile: 64 key rows x 256 B (16 chunks of 8 d); chunk c of
+// row r at c ^ (r & 15).  V tile: 128 d rows x 128 B (8 chunks of 8 stored key
+// positions); chunk c of row d at c ^ ((d >> 1) & 7).
+__device__ __forceinline__ int kswz(int r) { return r & 15; }
+__device__ __forceinline__ int vswz(int d) { return (d >> 1) & 7; }
+
+template <int DT, int REP, int PS>
+__global__ void __launch_bounds__(NS * REP * 2 * 64) attention_kernel(const AttnParams p) {
+  constexpr int GW = REP * 2;        // waves per split group
+  constexpr int KTILE = KB * HD * 2;  // 16 KB
+  constexpr int VTILE = HD * KB * 2;  // 16 KB
+  constexpr int STAGE = KTILE + VTILE;
+  constexpr int KI = KB * HD * 2 / 1024 / GW;  // K DMA instructions per wave per block
+  constexpr int VI = HD * KB * 2 / 1024 / GW;  // V DMA instructions per wave per block
+  constexpr int LPS = KI + VI;
+  static_assert(KI * GW * 4 == KB && VI * GW * 8 == HD, "DMA row coverage");
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[NS * 2 * STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int split = wave / GW, wg = wave % GW;
+  const int hh = wg / 2, rg = wg & 1;
+  const int fr = lane & 31, fh = lane >> 5;
+
+  const int T = (int)((p.rows + QT - 1) / QT);
+  const int t = T - 1 - (int)blockIdx.x;  // longest key ranges first
+  const int kvh = blockIdx.y;
+  const int head = kvh * REP + hh;
+  const int64_t row0 = (int64_t)t * QT;
+  const int64_t kend = p.q0 + min(row0 + QT, p.rows);  // keys 0..kend-1 are visible
+  const int nkb = (int)((kend + KB - 1) / KB);
+  const int iters = (nkb + NS - 1) / NS;
+
+  // ---- DMA addressing (the group's GW waves share each tile) ----
+  const uint16_t* kbase = p.k_cache + (int64_t)kvh * p.cap * HD;
+  const uint16_t* vbase = p.v_cache + (int64_t)kvh * HD * p.cap;
+  const __amdgpu_buffer_rsrc_t rsk = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(kbase), (short)0, (int)(p.cap * HD * 2), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rsv = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(vbase), (short)0, (int)(p.cap * HD * 2), 0x00020000);
+  auto issue = [&](int kb, int stage) {
+    unsigned char* sk = smem + (split * 2 + stage) * STAGE;
+    unsigned char* sv = sk + KTILE;
+#pragma unroll
+    for (int j = 0; j < KI; ++j) {
+      const int ins = j * GW + wg;            // 16 instructions, 4 key rows each
+      const int r = ins * 4 + (lane >> 4);    // key row within the tile
+      const int pc = lane & 15;
+      const int64_t key = (int64_t)kb * KB + r;
+      const uint32_t off =
+          key < p.cap ? (uint32_t)((key * HD + ((pc ^ kswz(r)) << 3)) * 2) : OOB;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsk, (QA_LDS void*)(sk + ins * 1024), 16, off, 0,
+                                               0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < VI; ++j) {
+      const int ins = j * GW + wg;            // 16 instructions, 8 d rows each
+      const int d = ins * 8 + (lane >> 3);
+      const int pc = lane & 7;
+      const int64_t col = (int64_t)kb * KB + ((pc ^ vswz(d)) << 3);
+      const uint32_t off = col < p.cap ? (uint32_t)(((int64_t)d * p.cap + col) * 2) : OOB;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsv, (QA_LDS void*)(sv + ins * 1024), 16, off, 0,
+                                               0, 0);
+    }
+  };
+
+  // ---- this wave's 32 query rows, as MFMA B fragments (8 slices of 16 d) ----
+  const int64_t qrow = row0 + rg * 32 + fr;
+  u32x4 qf[8];
+  {
+    const uint16_t* q = p.q + ((int64_t)head * p.rows + qrow) * HD + fh * 8;
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+      qf[s] = qrow < p.rows ? *reinterpret_cast<const u32x4*>(q + s * 16) : u32x4{0, 0, 0, 0};
+  }
+  const int64_t pos = p.q0 + qrow;  // this lane's query position
+  const float sc = p.scale * kLog2e;
+
+  f32x16 o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = f32x16{0};
+  float m_run = -INFINITY, l_run = 0.f;
+
+  auto compute = [&](int kb, int stage) {
+    const unsigned char* sk = smem + (split * 2 + stage) * STAGE;
+    const unsigned char* sv = sk + KTILE;
+    f32x16 s[2] = {f32x16{0}, f32x16{0}};
+#pragma unroll
+    for (int sl = 0; sl < 8; ++sl) {
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        const int r = kt * 32 + fr;
+        const u32x4 kf =
+            *reinterpret_cast<const u32x4*>(sk + r * 256 + (((2 * sl + fh) ^ kswz(r)) << 4));
+        s[kt] = AFmt<DT>::mfma(kf, qf[sl], s[kt]);
+      }
+    }
+    // scale, causal mask, row max (log2 domain)
+    float bm = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int64_t key = (int64_t)kb * KB + kt * 32 + 8 * g + 4 * fh + e;
+          const float x = key <= pos ? s[kt][4 * g + e] * sc : -INFINITY;
+          s[kt][4 * g + e] = x;
+          bm = fmaxf(bm, x);
+        }
+    bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+    const float m_new = fmaxf(m_run, bm);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+    const float m_b = m_use - AFmt<DT>::kPBias;
+    float rs = 0.f;
+    u32x4 pf[4], pl[4];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        float pv[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          pv[e] = __builtin_amdgcn_exp2f(s[kt][4 * g + e] - m_b);
+          rs += pv[e];
+        }
+        // slice j = 2 kt + g / 2 holds groups g = 2(j%2), 2(j%2)+1 of tile kt
+        const int j = 2 * kt + (g >> 1), half = g & 1;
+        uint32_t hi[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) hi[e] = AFmt<DT>::narrow(pv[e]);
+        pf[j][2 * half] = hi[0] | (hi[1] << 16);
+        pf[j][2 * half + 1] = hi[2] | (hi[3] << 16);
+        if constexpr (PS == 2) {  // the rounding residue as a second 16-bit term
+          uint32_t lo[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) lo[e] = AFmt<DT>::narrow(pv[e] - AFmt<DT>::widen(hi[e]));
+          pl[j][2 * half] = lo[0] | (lo[1] << 16);
+          pl[j][2 * half + 1] = lo[2] | (lo[3] << 16);
+        }
+      }
+    rs += __shfl_xor(rs, 32, 64);
+    l_run = l_run * alpha + rs;
+    m_run = m_new;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      const int d = dt * 32 + fr;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const u32x4 vf =
+            *reinterpret_cast<const u32x4*>(sv + d * 128 + (((2 * j + fh) ^ vswz(d)) << 4));
+        o[dt] = AFmt<DT>::mfma(vf, pf[j], o[dt]);
+        if constexpr (PS == 2) o[dt] = AFmt<DT>::mfma(vf, pl[j], o[dt]);
+      }
+    }
+  };
+
+  // ---- main loop: the split groups step through their key blocks in lockstep ----
+  const int kb0 = split;
+  if (kb0 < nkb) issue(kb0, 0);
+  if (kb0 + NS < nkb) issue(kb0 + NS, 1);
+  if (kb0 + NS < nkb)
+    wait_vmcnt<LPS>();
+  else
+    wait_vmcnt<0>();
+  exec_barrier();
+  for (int i = 0; i < iters; ++i) {
+    const int kb = kb0 + NS * i;
+    const int stage = i & 1;
+    if (kb < nkb) compute(kb, stage);
+    wait_lds();
+    exec_barrier();  // every wave is done with this stage's tiles
+    const bool refill = kb + 2 * NS < nkb;
+    if (refill) issue(kb + 2 * NS, stage);
+    if (i + 1 < iters) {
+      if (refill)
+        wait_vmcnt<LPS>();
+      else
+        wait_vmcnt<0>();
+      exec_barrier();  // the next stage has landed for every wave
+    }
+  }
+
+  // ---- merge the two key splits (fixed order) and write the output ----
+  __syncthreads();
+  float* xch = reinterpret_cast<float*>(smem);  // [GW waves][66 values][64 lanes]
+  if (split == 1) {
+    float* dst = xch + (size_t)wg * 66 * 64 + lane;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) dst[(dt * 16 + v) * 64] = o[dt][v];
+    dst[64 * 64] = m_run;
+    dst[65 * 64] = l_run;
+  }
+  __syncthreads();
+  if (split == 0 && qrow < p.rows) {
+    const float* src = xch + (size_t)wg * 66 * 64 + lane;
+    const float m1 = src[64 * 64], l1 = src[65 * 64];
+    const float mm = fmaxf(m_run, m1);
+    const float mu = mm == -INFINITY ? 0.f : mm;
+    const float a0 = __builtin_amdgcn_exp2f(m_run - mu), a1 = __builtin_amdgcn_exp2f(m1 - mu);
+    const float inv = 1.0f / (l_run * a0 + l1 * a1);
+    uint16_t* out = p.out + qrow * p.ldo + (int64_t)head * HD;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          v[e] = (o[dt][4 * g + e] * a0 + src[(dt * 16 + 4 * g + e) * 64] * a1) * inv;
+        const u32x2 pk = {AFmt<DT>::narrow(v[0]) | (AFmt<DT>::narrow(v[1]) << 16),
+                          AFmt<DT>::narrow(v[2]) | (AFmt<DT>::narrow(v[3]) << 16)};
+        *reinterpret_cast<u32x2*>(out + dt * 32 + 8 * g + 4 * fh) = pk;
+      }
+  }
+}
+
+}  // namespace
+
+hipError_t launch_attention(int dtype, const AttnParams& p, bool p16, hipStream_t s) {
+  const int rep = p.nqh / p.nkvh;
+  const dim3 grid((unsigned)((p.rows + QT - 1) / QT), (unsigned)p.nkvh);
+  const dim3 block(NS * rep * 2 * 64);
+  void (*k)(AttnParams) = nullptr;
+#define QA_ATTN_PICK(R)                                                                      \
+  if (dtype == QA_BF16)                                                                      \
+    k = p16 ? attention_kernel<QA_BF16, R, 1> : attention_kernel<QA_BF16, R, 2>;             \
+  else                                                                                       \
+    k = p16 ? attention_kernel<QA_F16, R, 1> : attention_kernel<QA_F16, R, 2>;
+  if (rep == 2) {
+    QA_ATTN_PICK(2)
+  } else if (rep == 1) {
+    QA_ATTN_PICK(1)
+  } else {
+    return hipErrorInvalidValue;  // rejected by qa_attention_prefill's validation
+  }
+#undef QA_ATTN_PICK
+  hipLaunchKernelGGL(k, grid, block, 0, s, p);
+  return hipGetLastError();
+}
+
+}  // namespace qa

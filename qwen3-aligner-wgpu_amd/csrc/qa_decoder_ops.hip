@@ -1,0 +1,175 @@
+// qa_decoder_ops.hip -- the decoder's prefill ops around the projections
+// that are not GEMMs: RMSNorm, and the per-head q/k RMSNorm + rotate-half
+// RoPE that writes the KV cache (the reference's `rms_norm` and
+// `qkv_extract` pipelines, src/decoder.rs:1305-1344,1610-1626; WGSL
+// src/shaders.rs:331-383,910-1031; CPU twin src/cpu_decoder.rs:288-322,464-491).
+//
+// All three are HBM-bound elementwise / row-reduction passes: one wave per
+// row (or per (row, head)), 16-byte loads and stores, f32 arithmetic, one
+// 16-bit rounding per output.  Rounding points follow the CPU path: the
+// norm's inverse RMS comes from the 16-bit input values in f32,
+// inv = 1 / sqrt(sum2 / n + eps) with IEEE sqrt and divide.
+#include "qa_internal.h"
+
+namespace qa {
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <int DT>
+__device__ __forceinline__ float widen16(uint32_t h) {
+  if constexpr (DT == QA_F16) return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+  else return __uint_as_float(h << 16);
+}
+template <int DT>
+__device__ __forceinline__ uint32_t narrow16(float v) {
+  if constexpr (DT == QA_F16) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v);
+  } else {
+    const uint32_t u = __float_as_uint(v);  // src/shaders.rs:169-179
+    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  }
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// y[r] = r16(x[r] * inv * w), one wave per row, 8 elements per lane per step.
+template <int DT>
+__global__ void __launch_bounds__(256) rms_norm_kernel(const RmsParams p) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= p.rows) return;
+  const uint16_t* x = p.x + r * p.ldx;
+  float s = 0.f;
+  for (int i = lane * 8; i < p.n; i += 512) {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(x + i);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float lo = widen16<DT>(v[e] & 0xffffu), hi = widen16<DT>(v[e] >> 16);
+      s += lo * lo;
+      s += hi * hi;
+    }
+  }
+  s = wave_sum(s);
+  const float inv = 1.0f / sqrtf(s / (float)p.n + p.eps);
+  uint16_t* y = p.y + r * p.ldy;
+  for (int i = lane * 8; i < p.n; i += 512) {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(x + i);
+    u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float lo = widen16<DT>(v[e] & 0xffffu) * inv * p.w[i + 2 * e];
+      const float hi = widen16<DT>(v[e] >> 16) * inv * p.w[i + 2 * e + 1];
+      o[e] = narrow16<DT>(lo) | (narrow16<DT>(hi) << 16);
+    }
+    *reinterpret_cast<u32x4*>(y + i) = o;
+  }
+}
+
+// One wave per (row, head slot): slots 0..nqh-1 are q heads (-> q_out
+// head-major [nqh][rows][hd]), nqh..nqh+nkvh-1 k heads (-> k_cache
+// [nkvh][cap][hd] at row start + r).  Lane l owns the rotate-half pairs
+// (j, j + hd/2) for j = l, l + 64, ..., so both partners of every rotation
+// are in one lane.
+template <int DT>
+__global__ void __launch_bounds__(256) qk_norm_rope_kernel(const RopeParams p) {
+  const int lane = threadIdx.x & 63;
+  const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int slots = p.nqh + p.nkvh;
+  if (item >= p.rows * slots) return;
+  const int64_t r = item / slots;
+  const int slot = (int)(item % slots);
+  const bool is_q = slot < p.nqh;
+  const int head = is_q ? slot : slot - p.nqh;
+  const int hd = p.hd, half = hd / 2;
+  const uint16_t* raw = p.qkv + r * p.ldqkv + (is_q ? 0 : (int64_t)p.nqh * hd) + (int64_t)head * hd;
+  const float* nw = is_q ? p.qn : p.kn;
+  const float* cs = p.cos + (p.pos0 + r) * hd;
+  const float* sn = p.sin + (p.pos0 + r) * hd;
+  uint16_t* dst = is_q ? p.q_out + ((int64_t)head * p.rows + r) * hd
+                       : p.k_cache + ((int64_t)head * p.cap + p.start + r) * hd;
+  float s = 0.f;
+  for (int j = lane; j < half; j += 64) {
+    const float a = widen16<DT>(raw[j]), b = widen16<DT>(raw[j + half]);
+    s += a * a;
+    s += b * b;
+  }
+  s = wave_sum(s);
+  const float inv = 1.0f / sqrtf(s / (float)hd + p.eps);
+  for (int j = lane; j < half; j += 64) {
+    const int k = j + half;
+    const float xj = widen16<DT>(raw[j]) * inv * nw[j];
+    const float xk = widen16<DT>(raw[k]) * inv * nw[k];
+    dst[j] = (uint16_t)narrow16<DT>(xj * cs[j] - xk * sn[j]);
+    dst[k] = (uint16_t)narrow16<DT>(xk * cs[k] + xj * sn[k]);
+  }
+}
+
+// Column of key t in the transposed V cache: bits 2 and 3 of t swapped, so
+// each aligned group of 16 keys is stored 0-3, 8-11, 4-7, 12-15 -- the key
+// order in which the attention kernel's P.V fragments hold them.
+__device__ __forceinline__ int64_t vperm(int64_t t) {
+  return (t & ~(int64_t)12) | ((t & 4) << 1) | ((t & 8) >> 1);
+}
+
+// V heads into the transposed cache v_cache[h][d][vperm(start + r)] through a
+// 64 (rows) x 64 (d) LDS tile, so the row reads are contiguous and the
+// transposed writes stay within 32-byte groups.
+template <int DT>
+__global__ void __launch_bounds__(256) v_transpose_kernel(const RopeParams p) {
+  __shared__ uint16_t tile[64][66];
+  const int64_t r0 = (int64_t)blockIdx.x * 64;
+  const int d0 = blockIdx.y * 64;
+  const int h = blockIdx.z;
+  const int t = threadIdx.x;
+  const uint16_t* v = p.qkv + (int64_t)(p.nqh + p.nkvh) * p.hd + (int64_t)h * p.hd + d0;
+  {
+    const int rr = t >> 2, c = (t & 3) * 16;
+    const int64_t r = r0 + rr;
+    if (r < p.rows) {
+      const uint16_t* src = v + r * p.ldqkv + c;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) tile[rr][c + e] = src[e];
+    }
+  }
+  __syncthreads();
+  {
+    const int dd = t >> 2, c = (t & 3) * 16;
+    uint16_t* dst = p.v_cache + ((int64_t)h * p.hd + d0 + dd) * p.cap;
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+      if (r0 + c + e < p.rows) dst[vperm(p.start + r0 + c + e)] = tile[c + e][dd];
+  }
+}
+
+}  // namespace
+
+hipError_t launch_rms_norm(int dtype, const RmsParams& p, hipStream_t s) {
+  const unsigned blocks = (unsigned)((p.rows + 3) / 4);
+  if (dtype == QA_BF16)
+    hipLaunchKernelGGL(rms_norm_kernel<QA_BF16>, dim3(blocks), dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL(rms_norm_kernel<QA_F16>, dim3(blocks), dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_qk_norm_rope(int dtype, const RopeParams& p, hipStream_t s) {
+  const int64_t items = p.rows * (p.nqh + p.nkvh);
+  const dim3 vt((unsigned)((p.rows + 63) / 64), (unsigned)(p.hd / 64), (unsigned)p.nkvh);
+  if (dtype == QA_BF16) {
+    hipLaunchKernelGGL(qk_norm_rope_kernel<QA_BF16>, dim3((unsigned)((items + 3) / 4)), dim3(256),
+                       0, s, p);
+    hipLaunchKernelGGL(v_transpose_kernel<QA_BF16>, vt, dim3(256), 0, s, p);
+  } else {
+    hipLaunchKernelGGL(qk_norm_rope_kernel<QA_F16>, dim3((unsigned)((items + 3) / 4)), dim3(256),
+                       0, s, p);
+    hipLaunchKernelGGL(v_transpose_kernel<QA_F16>, vt, dim3(256), 0, s, p);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace qa

@@ -72,5 +72,38 @@ struct Plan {
 hipError_t launch_gemm(int dtype, const Plan& plan, const GemmParams& p, int batch,
                        hipStream_t stream);
 
+// qa_rms_norm (qa_decoder_ops.hip).
+struct RmsParams {
+  const uint16_t* x;
+  const float* w;
+  uint16_t* y;
+  int64_t rows, ldx, ldy;
+  int n;
+  float eps;
+};
+hipError_t launch_rms_norm(int dtype, const RmsParams& p, hipStream_t stream);
+
+// qa_qk_norm_rope (qa_decoder_ops.hip).
+struct RopeParams {
+  const uint16_t* qkv;
+  const float *qn, *kn, *cos, *sin;
+  uint16_t *q_out, *k_cache, *v_cache;
+  int64_t rows, ldqkv, pos0, cap, start;
+  int nqh, nkvh, hd;
+  float eps;
+};
+hipError_t launch_qk_norm_rope(int dtype, const RopeParams& p, hipStream_t stream);
+
+// qa_attention_prefill (qa_attention.hip).
+struct AttnParams {
+  const uint16_t *q, *k_cache, *v_cache;
+  uint16_t* out;
+  int64_t rows, cap, q0, ldo;
+  int nqh, nkvh, hd;
+  float scale;
+};
+// p16: probabilities rounded once to the 16-bit format (else two 16-bit terms).
+hipError_t launch_attention(int dtype, const AttnParams& p, bool p16, hipStream_t stream);
+
 
 }  // namespace qa

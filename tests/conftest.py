@@ -145,3 +145,102 @@ def assert_silu_mul(got_bits, want_bits, a_bits, w_bits, gu_exact_bits, orc, dty
     assert excess.max() <= 0, (s, worst, got[worst], want[worst], bound[worst])
     assert s["identical"] >= min_identical, s
     return s
+
+
+# Rounding of the probabilities before the P.V product, per attention mode:
+# (relative, absolute) error per weight, for (f16, bf16).
+#   split: p (scaled by 2^15 for f16) enters as two 16-bit terms, value and
+#          rounding residue: the residue's own rounding, 2^-11 * 2^-11 (f16) or
+#          2^-8 * 2^-8 (bf16) relative; subnormal residues cost 2^-25 * 2^-15.
+#   p16:   p (scaled by 2^15 for f16) rounded once: 2^-11 / 2^-8 relative.
+#   p16_unscaled: p in [0, 1] rounded once (the reference GPU path's
+#          normalised 16-bit probabilities): f16 subnormals below 2^-14 add
+#          2^-25 absolute.
+P_ROUNDING = {
+    "split": ((2.0 ** -22, 2.0 ** -40), (2.0 ** -16, 0.0)),
+    "p16": ((2.0 ** -11, 2.0 ** -40), (2.0 ** -8, 0.0)),
+    "p16_unscaled": ((2.0 ** -11, 2.0 ** -25), (2.0 ** -8, 0.0)),
+}
+
+
+def attention_bound(q_bits, kc_bits, vc_bits, q0, want_bits, orc, dtype, mode="split"):
+    """Elementwise bound on |out_gpu - out_ref| for causal GQA attention.
+
+    Both sides compute s = q.k / sqrt(hd) in f32, p = exp(s - max) and
+    out = r(sum_t p_t v_t / sum_t p_t) with one 16-bit rounding r.  They may
+    differ by
+      * the f32 score error: each side's dot product is within
+        (hd + 16) 2^-24 sum_i |q_i k_i| / sqrt(hd) of the exact score (a
+        gamma_n bound covering both the 4-way partial sums and the MFMA
+        chain), and the exp argument's roundings (4 2^-24 |s| log2 e); a
+        score perturbation d moves every normalised weight by a factor
+        within exp(+-2d), so the weighted mean by expm1(2d) sum_t w_t |v_t|;
+      * P rounded to the 16-bit format before the P.V product, as `mode`
+        says (P_ROUNDING): relative u_p times sum_t w_t |v_t|, absolute
+        u_abs times sum_t |v_t| / sum_t p_t;
+      * the f32 accumulation over the kend visible keys on each side,
+        (2 kend + 16) 2^-24 sum_t w_t |v_t|, and the exp / merge roundings,
+        2^-20 relative;
+      * the final rounding of each side: one ulp of the result.
+    q [nqh, rows, hd], k cache [nkvh, cap, hd], transposed V cache
+    [nkvh, hd, cap] (key t at column vperm(t)), bits of the 16-bit format."""
+    q = orc.h16_to_f32(q_bits, dtype).astype(np.float64)
+    kf = orc.h16_to_f32(kc_bits, dtype).astype(np.float64)
+    vf = orc.h16_to_f32(vc_bits, dtype).astype(np.float64)
+    nqh, rows, hd = q.shape
+    nkvh, cap, _ = kf.shape
+    rep = nqh // nkvh
+    kend = q0 + rows
+    vf = vf[:, :, orc.vperm(cap)[:kend]]  # [nkvh, hd, key]
+    scale = 1.0 / np.sqrt(hd)
+    u_p, u_abs = P_ROUNDING[mode][dtype]
+    gam = (hd + 16) * 2.0 ** -24
+    acc = (2 * kend + 16) * 2.0 ** -24 + 2.0 ** -20
+    vis = np.arange(kend)[None, :] <= (q0 + np.arange(rows))[:, None]
+    bound = np.zeros((rows, nqh * hd))
+    for h in range(nqh):
+        kh = h // rep
+        s = q[h] @ kf[kh, :kend].T * scale
+        sabs = np.abs(q[h]) @ np.abs(kf[kh, :kend]).T * scale
+        s = np.where(vis, s, -np.inf)
+        p = np.exp(s - s.max(axis=1, keepdims=True))
+        z = p.sum(axis=1, keepdims=True)
+        smax = np.where(vis, np.abs(s), 0.0).max(axis=1, keepdims=True)
+        d = gam * np.where(vis, sabs, 0.0).max(axis=1, keepdims=True) + 6 * 2.0 ** -24 * smax
+        va = np.abs(vf[kh]).T  # [key, hd]
+        wabs = (p @ va) / z
+        bound[:, h * hd:(h + 1) * hd] = ((u_p + np.expm1(2 * d) + acc) * wabs
+                                         + u_abs * (vis.astype(np.float64) @ va) / z)
+    want = orc.h16_to_f32(want_bits, dtype).astype(np.float64)
+    return bound + ulp16(np.abs(want) + bound, dtype)
+
+
+def assert_attention(got_bits, want_bits, q_bits, kc_bits, vc_bits, q0, orc, dtype, mode="split"):
+    """Attention output against the oracle: finite, the north star's mean
+    absolute error (and, in the default split mode, its max relative error),
+    and the derived elementwise bound (attention_bound)."""
+    s = parity_stats(got_bits, want_bits, orc, dtype)
+    assert s["finite"], s
+    assert s["mae"] <= MAE_TOL, s
+    if mode == "split":
+        assert s["max_rel"] <= REL_TOL, s
+    bound = attention_bound(q_bits, kc_bits, vc_bits, q0, want_bits, orc, dtype, mode)
+    got = orc.h16_to_f32(got_bits, dtype).astype(np.float64)
+    want = orc.h16_to_f32(want_bits, dtype).astype(np.float64)
+    excess = np.abs(got - want) - bound
+    worst = np.unravel_index(np.argmax(excess), excess.shape)
+    assert excess.max() <= 0, (s, worst, got[worst], want[worst], bound[worst])
+    s["bound_use"] = float((np.abs(got - want) / bound).max())
+    return s
+
+
+def rope_tables(rows, hd, pos0, theta=1e6):
+    """cos/sin [pos][hd] as src/mrope.rs:55-82 builds them for text positions:
+    angle(pos, j) = pos * theta^(-2j/hd), the second half repeating the first."""
+    half = hd // 2
+    inv = 1.0 / theta ** (2.0 * np.arange(half) / hd)
+    pos = np.arange(pos0 + rows, dtype=np.float64)[:, None]
+    ang = pos * inv[None, :]
+    c = np.concatenate([np.cos(ang), np.cos(ang)], axis=1).astype(np.float32)
+    s = np.concatenate([np.sin(ang), np.sin(ang)], axis=1).astype(np.float32)
+    return c, s

@@ -104,6 +104,38 @@ def test_calls_without_context_fail_cleanly(pkg):
     assert lib.qa_sync(None) == pkg.QA_EINVAL
     assert lib.qa_ctx_destroy(None) == pkg.QA_OK
     assert lib.qa_ctx_create(0, None) == pkg.QA_EINVAL
+    for fn, desc in ((lib.qa_rms_norm, pkg.RmsNormDesc()), (lib.qa_qk_norm_rope, pkg.QkRopeDesc()),
+                     (lib.qa_attention_prefill, pkg.AttentionDesc())):
+        assert fn(None, ctypes.byref(desc)) == pkg.QA_EINVAL
+        assert "null argument" in pkg.last_error()
+
+
+def test_decoder_descriptor_layouts(pkg):
+    """The ctypes mirrors have the C structs' sizes and field offsets (checked
+    against a tiny C program compiled from include/qa.h)."""
+    import shutil
+    import tempfile
+    if not shutil.which("gcc"):
+        pytest.skip("gcc not available")
+    structs = {"qa_rms_norm_desc": pkg.RmsNormDesc, "qa_qk_rope_desc": pkg.QkRopeDesc,
+               "qa_attention_desc": pkg.AttentionDesc, "qa_linear_desc": pkg.LinearDesc,
+               "qa_mlp_desc": pkg.MlpDesc}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "qa.h"', "int main(void) {"]
+    for cname, py in structs.items():
+        lines.append(f'printf("{cname} %zu\\n", sizeof({cname}));')
+        for fname, _ in py._fields_:
+            lines.append(f'printf("{cname}.{fname} %zu\\n", offsetof({cname}, {fname}));')
+    lines.append("return 0; }")
+    with tempfile.TemporaryDirectory() as td:
+        src, exe = os.path.join(td, "l.c"), os.path.join(td, "l")
+        open(src, "w").write("\n".join(lines))
+        subprocess.run(["gcc", "-I", os.path.join(ROOT, "include"), src, "-o", exe], check=True)
+        got = dict(l.split() for l in subprocess.run([exe], capture_output=True, text=True,
+                                                     check=True).stdout.splitlines())
+    for cname, py in structs.items():
+        assert int(got[cname]) == ctypes.sizeof(py), cname
+        for fname, _ in py._fields_:
+            assert int(got[f"{cname}.{fname}"]) == getattr(py, fname).offset, (cname, fname)
 
 
 def test_no_device_is_a_typed_error():

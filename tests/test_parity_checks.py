@@ -6,13 +6,21 @@ plausible mistakes of a fused SiLU.up epilogue: gate and up swapped, the up
 half paired one column off, and the intermediate 16-bit roundings of g and u
 skipped (one rounding of silu(g) * u instead of three).  The mistakes are
 planted in CPU-side results built from the oracle's pieces.
+
+The attention check is pinned the same way: it accepts the GPU kernel's
+arithmetic in both modes (unnormalised probabilities, scaled by 2^15 for f16,
+entering the P.V product as two 16-bit terms or rounded once) and the
+reference GPU path's (normalised, then rounded), each emulated here in f64
+with the probabilities rounded as that arithmetic rounds them, and rejects a
+causal bound one key too far, a missing 1/sqrt(hd), a wrong q-head -> kv-head
+map and an unpermuted V cache.
 """
 from __future__ import annotations
 
 import numpy as np
 import pytest
 
-from conftest import assert_silu_mul, ulp16
+from conftest import REL_TOL, assert_attention, assert_silu_mul, parity_stats, ulp16
 
 
 def _case(orc, dtype, m=64, inter=256, hidden=512, seed=3):
@@ -73,3 +81,79 @@ def test_silu_check_rejects_mistakes(orc, dtype, mistake):
     rel = 1e-2 if dtype == 0 else 0.03
     with pytest.raises(AssertionError):
         assert_silu_mul(bad, exact, a, w, gu_exact, orc, dtype, k, rel_tol=rel)
+
+
+def _attn_inputs(orc, dtype, rows=40, q0=24, nqh=4, nkvh=2, hd=128, cap=80, seed=5):
+    rng = np.random.default_rng(seed)
+    h16 = lambda x: orc.h16_from_f32(x.astype(np.float32), dtype)  # noqa: E731
+    q = h16(1.5 * rng.standard_normal((nqh, rows, hd)))
+    kc = h16(rng.standard_normal((nkvh, cap, hd)))
+    vc = h16(rng.standard_normal((nkvh, hd, cap)))
+    return q, kc, vc, q0
+
+
+def _attn_emulate(orc, dtype, q, kc, vc, q0, *, mode="split", causal_shift=0,
+                  scale=None, kv_of=None, permute=True):
+    """f64 attention with the probabilities rounded to the 16-bit format as
+    `mode` says (conftest.P_ROUNDING)."""
+    f = lambda b: orc.h16_to_f32(b, dtype).astype(np.float64)  # noqa: E731
+    qf, kf, vf = f(q), f(kc), f(vc)
+    nqh, rows, hd = qf.shape
+    nkvh, cap, _ = kf.shape
+    cols = orc.vperm(cap) if permute else np.arange(cap)
+    vf = vf[:, :, cols]
+    scale = 1.0 / np.sqrt(hd) if scale is None else scale
+    kv_of = (lambda h: h // (nqh // nkvh)) if kv_of is None else kv_of
+    vis = np.arange(cap)[None, :] <= (q0 + np.arange(rows) + causal_shift)[:, None]
+    out = np.zeros((rows, nqh * hd))
+    r16 = lambda x: f(orc.h16_from_f32(x.astype(np.float32), dtype))  # noqa: E731
+    for h in range(nqh):
+        kh = kv_of(h)
+        s = np.where(vis, qf[h] @ kf[kh].T * scale, -np.inf)
+        p = np.exp(s - s.max(axis=1, keepdims=True))
+        z = p.sum(axis=1, keepdims=True)
+        if mode == "p16_unscaled":
+            o = r16(p / z) @ vf[kh].T
+        else:
+            ps = (p * (2.0 ** 15 if dtype == 0 else 1.0)).astype(np.float32)
+            pr = r16(ps)
+            if mode == "split":
+                pr = pr + r16((ps - pr.astype(np.float32)).astype(np.float64))
+            o = (pr @ vf[kh].T) / (z * (2.0 ** 15 if dtype == 0 else 1.0))
+        out[:, h * hd:(h + 1) * hd] = o
+    return orc.h16_from_f32(out.astype(np.float32), dtype)
+
+
+@pytest.mark.parametrize("dtype", [0, 1], ids=["f16", "bf16"])
+@pytest.mark.parametrize("mode", ["split", "p16", "p16_unscaled"])
+def test_attention_check_accepts_rounded_probabilities(orc, dtype, mode):
+    q, kc, vc, q0 = _attn_inputs(orc, dtype)
+    want = orc.attention(dtype, q, kc, vc, q0)
+    got = _attn_emulate(orc, dtype, q, kc, vc, q0, mode=mode)
+    assert_attention(got, want, q, kc, vc, q0, orc, dtype, mode=mode)
+
+
+@pytest.mark.parametrize("dtype", [0, 1], ids=["f16", "bf16"])
+def test_attention_single_rounding_misses_the_north_star(orc, dtype):
+    """Why the split is the default: one 16-bit rounding of the probabilities
+    already exceeds the north star's max relative error on outputs near the
+    relative-error floor, while the split stays within one 16-bit ulp."""
+    q, kc, vc, q0 = _attn_inputs(orc, dtype, rows=120, q0=200, cap=320)
+    want = orc.attention(dtype, q, kc, vc, q0)
+    single = parity_stats(_attn_emulate(orc, dtype, q, kc, vc, q0, mode="p16"), want, orc, dtype)
+    split = parity_stats(_attn_emulate(orc, dtype, q, kc, vc, q0, mode="split"), want, orc, dtype)
+    assert single["max_rel"] > REL_TOL and split["max_rel"] <= REL_TOL, (single, split)
+    assert split["max_ulp"] <= 1 and split["identical"] >= 0.99, split
+
+
+@pytest.mark.parametrize("dtype", [0, 1], ids=["f16", "bf16"])
+@pytest.mark.parametrize("mode", ["split", "p16"])
+@pytest.mark.parametrize("mistake", ["causal_plus_one", "no_scale", "kv_head_map", "v_unpermuted"])
+def test_attention_check_rejects_mistakes(orc, dtype, mode, mistake):
+    q, kc, vc, q0 = _attn_inputs(orc, dtype)
+    want = orc.attention(dtype, q, kc, vc, q0)
+    kw = {"causal_plus_one": dict(causal_shift=1), "no_scale": dict(scale=1.0),
+          "kv_head_map": dict(kv_of=lambda h: h % 2), "v_unpermuted": dict(permute=False)}[mistake]
+    bad = _attn_emulate(orc, dtype, q, kc, vc, q0, mode=mode, **kw)
+    with pytest.raises(AssertionError):
+        assert_attention(bad, want, q, kc, vc, q0, orc, dtype, mode=mode)
