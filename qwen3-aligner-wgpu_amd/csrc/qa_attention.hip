@@ -43,6 +43,9 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 #define QA_LDS __attribute__((address_space(3)))
 
@@ -61,11 +64,12 @@ struct AFmt<QA_F16> {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
   }
-  __device__ static __forceinline__ uint32_t narrow(float v) {
-    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v);
+  // two values, RNE, element a in the low half (v_cvt_pk_f16_f32)
+  __device__ static __forceinline__ uint32_t pack2(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, f16x2));
   }
-  __device__ static __forceinline__ float widen(uint32_t h) {
-    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+  __device__ static __forceinline__ f32x2 unpack2(uint32_t h) {
+    return __builtin_convertvector(__builtin_bit_cast(f16x2, h), f32x2);
   }
   // Probabilities are formed as p * 2^15 (<= 32768): the f16 range keeps them
   // normal down to p = 2^-29, so rounding them loses only relative precision.
@@ -77,11 +81,14 @@ struct AFmt<QA_BF16> {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
   }
-  __device__ static __forceinline__ uint32_t narrow(float v) {  // src/shaders.rs:169-179
-    const uint32_t u = __float_as_uint(v);
-    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  // two values, RNE (v_cvt_pk_bf16_f32): for finite values the reference's
+  // (u + 0x7fff + ((u >> 16) & 1)) >> 16, src/shaders.rs:169-179
+  __device__ static __forceinline__ uint32_t pack2(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, bf16x2));
   }
-  __device__ static __forceinline__ float widen(uint32_t h) { return __uint_as_float(h << 16); }
+  __device__ static __forceinline__ f32x2 unpack2(uint32_t h) {
+    return (f32x2){__uint_as_float(h << 16), __uint_as_float(h & 0xffff0000u)};
+  }
   static constexpr float kPBias = 0.f;
 };
 
@@ -176,7 +183,8 @@ __global__ void __launch_bounds__(NS * REP * 2 * 64) attention_kernel(const Attn
     for (int s = 0; s < 8; ++s)
       qf[s] = qrow < p.rows ? *reinterpret_cast<const u32x4*>(q + s * 16) : u32x4{0, 0, 0, 0};
   }
-  const int64_t pos = p.q0 + qrow;  // this lane's query position
+  const int pos = (int)(p.q0 + qrow);                   // this lane's query position
+  const int wpos0 = (int)(p.q0 + row0 + rg * 32);       // the wave's first position
   const float sc = p.scale * kLog2e;
 
   f32x16 o[4];
@@ -198,21 +206,25 @@ __global__ void __launch_bounds__(NS * REP * 2 * 64) attention_kernel(const Attn
         s[kt] = AFmt<DT>::mfma(kf, qf[sl], s[kt]);
       }
     }
-    // scale, causal mask, row max (log2 domain)
+    // causal mask, only in blocks that cross this wave's diagonal
+    if (kb * KB + KB - 1 > wpos0) {
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (kb * KB + kt * 32 + 8 * g + 4 * fh + e > pos) s[kt][4 * g + e] = -INFINITY;
+    }
+    // row max of the raw scores; the scale (> 0) is applied to the max and,
+    // fused, in the exponent: exp2(s sc - m)
     float bm = -INFINITY;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int g = 0; g < 4; ++g)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int64_t key = (int64_t)kb * KB + kt * 32 + 8 * g + 4 * fh + e;
-          const float x = key <= pos ? s[kt][4 * g + e] * sc : -INFINITY;
-          s[kt][4 * g + e] = x;
-          bm = fmaxf(bm, x);
-        }
+      for (int i = 0; i < 16; ++i) bm = fmaxf(bm, s[kt][i]);
     bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
-    const float m_new = fmaxf(m_run, bm);
+    const float m_new = fmaxf(m_run, bm * sc);
     const float m_use = m_new == -INFINITY ? 0.f : m_new;
     const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
     const float m_b = m_use - AFmt<DT>::kPBias;
@@ -225,29 +237,27 @@ __global__ void __launch_bounds__(NS * REP * 2 * 64) attention_kernel(const Attn
         float pv[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          pv[e] = __builtin_amdgcn_exp2f(s[kt][4 * g + e] - m_b);
+          pv[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][4 * g + e], sc, -m_b));
           rs += pv[e];
         }
         // slice j = 2 kt + g / 2 holds groups g = 2(j%2), 2(j%2)+1 of tile kt
         const int j = 2 * kt + (g >> 1), half = g & 1;
-        uint32_t hi[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) hi[e] = AFmt<DT>::narrow(pv[e]);
-        pf[j][2 * half] = hi[0] | (hi[1] << 16);
-        pf[j][2 * half + 1] = hi[2] | (hi[3] << 16);
+        pf[j][2 * half] = AFmt<DT>::pack2(pv[0], pv[1]);
+        pf[j][2 * half + 1] = AFmt<DT>::pack2(pv[2], pv[3]);
         if constexpr (PS == 2) {  // the rounding residue as a second 16-bit term
-          uint32_t lo[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) lo[e] = AFmt<DT>::narrow(pv[e] - AFmt<DT>::widen(hi[e]));
-          pl[j][2 * half] = lo[0] | (lo[1] << 16);
-          pl[j][2 * half + 1] = lo[2] | (lo[3] << 16);
+          const f32x2 h01 = AFmt<DT>::unpack2(pf[j][2 * half]);
+          const f32x2 h23 = AFmt<DT>::unpack2(pf[j][2 * half + 1]);
+          pl[j][2 * half] = AFmt<DT>::pack2(pv[0] - h01[0], pv[1] - h01[1]);
+          pl[j][2 * half + 1] = AFmt<DT>::pack2(pv[2] - h23[0], pv[3] - h23[1]);
         }
       }
     rs += __shfl_xor(rs, 32, 64);
     l_run = l_run * alpha + rs;
     m_run = m_new;
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {  // some row's max moved
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
+      for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
+    }
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
       const int d = dt * 32 + fr;
@@ -316,8 +326,7 @@ __global__ void __launch_bounds__(NS * REP * 2 * 64) attention_kernel(const Attn
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           v[e] = (o[dt][4 * g + e] * a0 + src[(dt * 16 + 4 * g + e) * 64] * a1) * inv;
-        const u32x2 pk = {AFmt<DT>::narrow(v[0]) | (AFmt<DT>::narrow(v[1]) << 16),
-                          AFmt<DT>::narrow(v[2]) | (AFmt<DT>::narrow(v[3]) << 16)};
+        const u32x2 pk = {AFmt<DT>::pack2(v[0], v[1]), AFmt<DT>::pack2(v[2], v[3])};
         *reinterpret_cast<u32x2*>(out + dt * 32 + 8 * g + 4 * fh) = pk;
       }
   }

@@ -140,9 +140,23 @@ __global__ void __launch_bounds__(256) v_transpose_kernel(const RopeParams p) {
   {
     const int dd = t >> 2, c = (t & 3) * 16;
     uint16_t* dst = p.v_cache + ((int64_t)h * p.hd + d0 + dd) * p.cap;
+    const int64_t k0 = p.start + r0 + c;  // cache position of this thread's first key
+    if ((k0 & 15) == 0 && r0 + c + 16 <= p.rows && (reinterpret_cast<uintptr_t>(dst) & 15) == 0) {
+      // a whole aligned group of 16 keys: store it permuted, as two 16-byte runs
+      uint32_t w[8];
 #pragma unroll
-    for (int e = 0; e < 16; ++e)
-      if (r0 + c + e < p.rows) dst[vperm(p.start + r0 + c + e)] = tile[c + e][dd];
+      for (int i = 0; i < 8; ++i) {
+        const int a = (int)vperm(2 * i), b = (int)vperm(2 * i + 1);  // stored column -> key
+        w[i] = (uint32_t)tile[c + a][dd] | ((uint32_t)tile[c + b][dd] << 16);
+      }
+      u32x4* out = reinterpret_cast<u32x4*>(dst + k0);
+      out[0] = u32x4{w[0], w[1], w[2], w[3]};
+      out[1] = u32x4{w[4], w[5], w[6], w[7]};
+    } else {
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        if (r0 + c + e < p.rows) dst[vperm(k0 + e)] = tile[c + e][dd];
+    }
   }
 }
 
