@@ -40,7 +40,8 @@ PEAK_F16_TFLOPS = 2516.6  # MI355X dense FP16/BF16 MFMA: 256 CU x 4096 FLOP/clk 
 PEAK_HBM_GBS = 8000.0
 METRIC = "GEMM TFLOP/s + % MFMA peak (f16, M=1024); aligner forward ms per 300 s audio"
 
-DEC = dict(layers=28, hidden=1024, q_dim=2048, kv_dim=1024, inter=3072)
+DEC = dict(layers=28, hidden=1024, q_dim=2048, kv_dim=1024, inter=3072, nqh=16, nkvh=8, hd=128)
+PREFILL_ROWS = (1024, 4352)  # config 3's M; config 5's ~300 s prefill (~4.3 k tokens)
 ENC = dict(layers=18, d_model=896, ffn=3584, conv_k=128 * 9)
 COPY_CAL_BYTES = 512 << 20
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemm_decoder_config3_traffic.json")
@@ -116,13 +117,20 @@ def cpu_baseline(orc, host, m, budget_s):
     }
 
 
-def bench_decoder(pkg, host, ctx, m, warmup, steps):
+def bench_decoder(pkg, host, ctx, m, warmup, steps, tdec=None):
+    """Config 3 (the headline).  When `tdec` (a host.TextDecoder) is given, the
+    same weights are loaded into it too, with unit norm weights."""
     dec = host.DecoderLinears(ctx, pkg.F16, DEC["layers"], m, DEC["hidden"], DEC["q_dim"],
                               DEC["kv_dim"], DEC["inter"])
     t0 = time.perf_counter()
+    ones_h = np.ones(DEC["hidden"], np.float32)
+    ones_d = np.ones(DEC["hd"], np.float32)
     for li in range(DEC["layers"]):
         w = decoder_weights(host, li)
         dec.load_layer(li, w["q"], w["k"], w["v"], w["o"], w["gate"], w["up"], w["down"])
+        if tdec is not None:
+            tdec.load_layer(li, w["q"], w["k"], w["v"], w["o"], w["gate"], w["up"], w["down"],
+                            ones_h, ones_h, ones_d, ones_d)
     dec.set_inputs(m, rmsnormed(host, 0, 1, (m, DEC["hidden"]), 0),
                    rmsnormed(host, 0, 2, (m, DEC["q_dim"]), 0),
                    rmsnormed(host, 0, 3, (m, DEC["hidden"]), 0),
@@ -131,6 +139,40 @@ def bench_decoder(pkg, host, ctx, m, warmup, steps):
     ev_ms, wall_ms = dec.time(m, warmup, steps, use_graph=True)
     sites = dec.profile_sites(m, max(2, steps // 4))
     return dec, ev_ms, wall_ms, sites
+
+
+def rope_tables(positions, hd, theta=1e6):
+    """Text-position RoPE tables cos/sin [positions][hd] (src/mrope.rs:55-82)."""
+    half = hd // 2
+    inv = 1.0 / theta ** (2.0 * np.arange(half) / hd)
+    ang = np.arange(positions, dtype=np.float64)[:, None] * inv[None, :]
+    return (np.concatenate([np.cos(ang)] * 2, axis=1).astype(np.float32),
+            np.concatenate([np.sin(ang)] * 2, axis=1).astype(np.float32))
+
+
+def dec_layer_flops(s):
+    """Per-layer FLOPs of a prefill of s tokens: the four projections plus the
+    causal attention (QK^T and PV over the s(s+1)/2 visible pairs per head)."""
+    per, _ = dec_flops(s)
+    attn = 4 * DEC["hd"] * DEC["nqh"] * s * (s + 1) // 2
+    return sum(per.values()), attn
+
+
+def bench_prefill(host, tdec, rows, warmup, steps):
+    """Whole decoder layers (norms, qkv, RoPE + KV write, attention, o,
+    gate|up + SiLU, down) over `rows` tokens, 28 layers, one hipGraph per step."""
+    h = rmsnormed(host, 2, 7, (rows, DEC["hidden"]), 0)
+    tdec.set_hidden(h)
+    ev_ms, wall_ms = tdec.time(rows, warmup, steps, use_graph=True)
+    ops = tdec.profile_ops(rows, 2)
+    lin_f, attn_f = dec_layer_flops(rows)
+    t_attn = ops["attention"]
+    return {
+        "ms": round(max(ev_ms, wall_ms), 3),
+        "tflops": round(DEC["layers"] * (lin_f + attn_f) / (max(ev_ms, wall_ms) * 1e-3) / 1e12, 1),
+        "per_layer_op_us": {k: round(v * 1e3, 2) for k, v in ops.items()},
+        "attention_tflops": round(attn_f / (t_attn * 1e-3) / 1e12, 1),
+    }
 
 
 def bench_encoder(pkg, host, ctx, m, warmup, steps):
@@ -185,7 +227,12 @@ def main():
     m = 1024
     ctx = pkg.Context(0)
     per, total_flops = dec_flops(m)
-    dec, ev_ms, wall_ms, sites = bench_decoder(pkg, host, ctx, m, args.warmup, args.steps)
+    tdec = None
+    if not args.no_detail:
+        tdec = host.TextDecoder(ctx, pkg.F16, DEC["layers"], max(PREFILL_ROWS), DEC["hidden"],
+                                DEC["nqh"], DEC["nkvh"], DEC["hd"], DEC["inter"])
+        tdec.set_rope(*rope_tables(max(PREFILL_ROWS), DEC["hd"]))
+    dec, ev_ms, wall_ms, sites = bench_decoder(pkg, host, ctx, m, args.warmup, args.steps, tdec)
     ms_per_step = max(ev_ms, wall_ms)
     value = total_flops / (ms_per_step * 1e-3) / 1e12
     gu_ms = sites["gu"]
@@ -225,6 +272,13 @@ def main():
         for b in (dx, dgu, dwd, dact):
             b.free()
     dec.close()
+    if tdec is not None:
+        # whole decoder layers: config 3's 1024 tokens and config 5's prefill length
+        for rows in PREFILL_ROWS:
+            r = bench_prefill(host, tdec, rows, 2, 5)
+            detail[f"decoder_prefill_{rows}"] = r
+            log(f"[bench] decoder prefill s={rows}: {r}")
+        tdec.close()
     if not args.no_detail:
         # config 4: 18-layer audio-tower linear stack, bf16, M=3750, + conv GEMM
         ev4, wall4, sites4, f4 = bench_encoder(pkg, host, ctx, 3750, 2, 5)

@@ -17,6 +17,7 @@
 #include <thread>
 
 #include "qa_host.h"
+#include "timing.hpp"
 
 namespace qa_host {
 
@@ -383,55 +384,6 @@ __global__ void copy_kernel(const uint4* __restrict__ src, uint4* __restrict__ d
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
        i += (size_t)gridDim.x * blockDim.x)
     dst[i] = src[i];
-}
-
-// Runs `step` warmup + steps times; optional graph capture of one step.
-template <class Step>
-int time_steps(qa_ctx* ctx, int warmup, int steps, int use_graph, Step&& step, double* ms,
-               double* wall_ms = nullptr) {
-  hipStream_t s = (hipStream_t)qa_ctx_stream(ctx);
-  for (int i = 0; i < warmup; ++i)
-    if (int rc = step()) return rc;
-  if (int rc = qa_sync(ctx)) return rc;
-  hipGraphExec_t exec = nullptr;
-  hipGraph_t graph = nullptr;
-  if (use_graph) {
-    if (hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal) != hipSuccess) return QA_EDEVICE;
-    const int rc = step();
-    const hipError_t ec = hipStreamEndCapture(s, &graph);
-    if (rc) return rc;
-    if (ec != hipSuccess) return QA_EDEVICE;
-    if (hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0) != hipSuccess) return QA_EDEVICE;
-    if (hipGraphLaunch(exec, s) != hipSuccess) return QA_EDEVICE;  // upload + warm
-    if (int rc2 = qa_sync(ctx)) return rc2;
-  }
-  hipEvent_t e0, e1;
-  (void)hipEventCreate(&e0);
-  (void)hipEventCreate(&e1);
-  const auto w0 = std::chrono::steady_clock::now();
-  (void)hipEventRecord(e0, s);
-  int rc = QA_OK;
-  for (int i = 0; i < steps && rc == QA_OK; ++i) {
-    if (exec)
-      rc = hip_status(hipGraphLaunch(exec, s));
-    else
-      rc = step();
-  }
-  (void)hipEventRecord(e1, s);
-  const int rs = qa_sync(ctx);
-  const auto w1 = std::chrono::steady_clock::now();
-  if (wall_ms && steps > 0)
-    *wall_ms = std::chrono::duration<double, std::milli>(w1 - w0).count() / steps;
-  float t = 0.f;
-  (void)hipEventElapsedTime(&t, e0, e1);
-  (void)hipEventDestroy(e0);
-  (void)hipEventDestroy(e1);
-  if (exec) (void)hipGraphExecDestroy(exec);
-  if (graph) (void)hipGraphDestroy(graph);
-  if (rc) return rc;
-  if (rs) return rs;
-  *ms = steps > 0 ? (double)t / steps : 0.0;
-  return QA_OK;
 }
 
 }  // namespace

@@ -14,8 +14,10 @@
  *     residual, :1594-1602 fc1 + bias + GELU, :1603-1605 fc2 + bias + residual)
  *     and a conv block as an im2col GEMM + bias + GELU
  *     (src/audio_encoder.rs:376-447, the CPU conv block).
- * The non-GEMM ops between them (norms, attention, RoPE) are not part of this
- * path; their outputs are fixed synthetic inputs here.
+ * The projection-only objects (qah_decoder, qah_encoder) take the non-GEMM
+ * ops' outputs as fixed synthetic inputs; qah_tdec runs whole decoder layers,
+ * norms, RoPE + KV-cache write and attention included
+ * (WgpuTextDecoder::prefill's layer loop, src/decoder.rs:1305-1657).
  *
  * It is not part of the product boundary (include/qa.h): a Rust caller keeps
  * its own host code and binds only include/qa.h.
@@ -106,6 +108,41 @@ int qah_encoder_time(qah_encoder* e, int rows, int warmup, int steps, int use_gr
 /* site_ms[0..4] = conv, qkv, o, fc1, fc2 */
 int qah_encoder_profile_sites(qah_encoder* e, int rows, int steps, double* site_ms);
 void qah_encoder_destroy(qah_encoder* e);
+
+/* ---- whole text-decoder layers (decoder_prefill.cpp) ---- */
+typedef struct qah_tdec qah_tdec;
+/* Qwen3 decoder: hidden, nqh x hd query heads over nkvh kv heads, SwiGLU MLP
+ * of width inter; RMSNorm epsilon eps; up to max_rows positions. */
+int qah_tdec_create(qa_ctx* ctx, int dtype, int layers, int hidden, int nqh, int nkvh, int hd,
+                    int inter, int max_rows, float eps, qah_tdec** out);
+/* Layer li: the seven projections as qah_decoder_load_layer, plus f32 norm
+ * weights iln, pln [hidden] (input / post-attention RMSNorm) and qn, kn [hd]
+ * (q / k head RMSNorm). */
+int qah_tdec_load_layer(qah_tdec* t, int li, const uint16_t* q, const uint16_t* k,
+                        const uint16_t* v, const uint16_t* o, const uint16_t* gate,
+                        const uint16_t* up, const uint16_t* down, const float* iln,
+                        const float* pln, const float* qn, const float* kn);
+/* RoPE tables cos / sin [positions][hd] (src/mrope.rs:55-82); a prefill of
+ * `rows` positions needs positions >= rows. */
+int qah_tdec_set_rope(qah_tdec* t, const float* cos, const float* sin, int positions);
+/* qa_attention_desc.flags used by the layers' attention (0 or QA_ATTN_P16). */
+int qah_tdec_set_attention_flags(qah_tdec* t, uint32_t flags);
+/* The residual stream h [rows, hidden] the first layer reads. */
+int qah_tdec_set_hidden(qah_tdec* t, int rows, const uint16_t* h);
+/* Enqueue every layer over positions 0..rows-1 (no wait); h is updated in place. */
+int qah_tdec_prefill(qah_tdec* t, int rows);
+/* which = 0 h [rows, hidden], 1 attn [rows, nqh hd], 2 qkv [rows, (nqh + 2 nkvh) hd],
+ * 3 act [rows, inter], 4 normed, 5 norm2 [rows, hidden], 6 q heads [nqh, rows, hd]
+ * of the last layer run; 7 K cache [nkvh, cap, hd] and 8 V cache (transposed,
+ * [nkvh, hd, cap]) of the last layer, cap = max_rows rounded up to 64. */
+int qah_tdec_read(qah_tdec* t, int which, int rows, uint16_t* host);
+int qah_tdec_time(qah_tdec* t, int rows, int warmup, int steps, int use_graph,
+                  double* ms_per_step, double* wall_ms_per_step);
+/* Average ms per layer of each op over `steps` prefills, every launch
+ * bracketed by its own HIP events: op_ms[0..7] = rms_norm, qkv, qk_norm_rope,
+ * attention, o, rms_norm 2, gate|up, down. */
+int qah_tdec_profile_ops(qah_tdec* t, int rows, int steps, double* op_ms);
+void qah_tdec_destroy(qah_tdec* t);
 
 /* Time `iters` back-to-back launches of one descriptor (HIP events around the
  * whole run on the context's stream); ms per launch. */

@@ -45,6 +45,19 @@ def declare(L: ctypes.CDLL) -> None:
     L.qah_encoder_profile_sites.argtypes = [_vp, _i, _i, _dp]
     L.qah_encoder_destroy.argtypes = [_vp]
     L.qah_encoder_destroy.restype = None
+    _fp = ctypes.POINTER(ctypes.c_float)
+    L.qah_tdec_create.argtypes = [_vp] + [_i] * 8 + [ctypes.c_float, ctypes.POINTER(_vp)]
+    L.qah_tdec_load_layer.argtypes = [_vp, _i] + [_vp] * 11
+    L.qah_tdec_set_rope.argtypes = [_vp, _vp, _vp, _i]
+    L.qah_tdec_set_attention_flags.argtypes = [_vp, ctypes.c_uint32]
+    L.qah_tdec_set_hidden.argtypes = [_vp, _i, _vp]
+    L.qah_tdec_prefill.argtypes = [_vp, _i]
+    L.qah_tdec_read.argtypes = [_vp, _i, _i, _vp]
+    L.qah_tdec_time.argtypes = [_vp, _i, _i, _i, _i, _dp, _dp]
+    L.qah_tdec_profile_ops.argtypes = [_vp, _i, _i, _dp]
+    L.qah_tdec_destroy.argtypes = [_vp]
+    L.qah_tdec_destroy.restype = None
+    del _fp
     L.qah_time_linear.argtypes = [_vp, _vp, _i, _i, _dp]
     L.qah_copy_calibration.argtypes = [_vp, _sz, _i]
     for name in ("qah_decoder_create", "qah_decoder_load_layer", "qah_decoder_set_inputs",
@@ -52,7 +65,10 @@ def declare(L: ctypes.CDLL) -> None:
                  "qah_decoder_profile_sites", "qah_encoder_create", "qah_encoder_load_layer",
                  "qah_encoder_load_conv", "qah_encoder_set_inputs", "qah_encoder_forward_linears",
                  "qah_encoder_read", "qah_encoder_time", "qah_encoder_profile_sites",
-                 "qah_time_linear", "qah_copy_calibration"):
+                 "qah_time_linear", "qah_copy_calibration", "qah_tdec_create",
+                 "qah_tdec_load_layer", "qah_tdec_set_rope", "qah_tdec_set_attention_flags",
+                 "qah_tdec_set_hidden", "qah_tdec_prefill", "qah_tdec_read", "qah_tdec_time",
+                 "qah_tdec_profile_ops"):
         getattr(L, name).restype = _i
 
 
@@ -193,6 +209,77 @@ class EncoderLinears:
         out = (ctypes.c_double * 5)()
         check(host_lib().qah_encoder_profile_sites(self.handle, rows, steps, out))
         return dict(zip(("conv", "qkv", "o", "fc1", "fc2"), list(out)))
+
+
+class TextDecoder:
+    """qah_tdec: whole Qwen3 decoder layers (norms, qkv, RoPE + KV write,
+    attention, o, gate|up + SiLU, down), WgpuTextDecoder::prefill's loop."""
+
+    OPS = ("rms_norm", "qkv", "qk_norm_rope", "attention", "o", "rms_norm2", "gu", "down")
+
+    def __init__(self, ctx, dtype: int, layers: int, max_rows: int, hidden: int = 1024,
+                 nqh: int = 16, nkvh: int = 8, hd: int = 128, inter: int = 3072,
+                 eps: float = 1e-6):
+        self.ctx, self.dtype, self.layers, self.max_rows = ctx, dtype, layers, max_rows
+        self.hidden, self.nqh, self.nkvh, self.hd, self.inter = hidden, nqh, nkvh, hd, inter
+        h = _vp()
+        check(host_lib().qah_tdec_create(ctx.handle, dtype, layers, hidden, nqh, nkvh, hd, inter,
+                                         max_rows, eps, ctypes.byref(h)))
+        self.handle = h.value
+
+    def close(self):
+        if self.handle:
+            host_lib().qah_tdec_destroy(self.handle)
+            self.handle = None
+
+    def load_layer(self, li, q, k, v, o, gate, up, down, iln, pln, qn, kn):
+        w16 = [np.ascontiguousarray(a, np.uint16) for a in (q, k, v, o, gate, up, down)]
+        w32 = [np.ascontiguousarray(a, np.float32) for a in (iln, pln, qn, kn)]
+        check(host_lib().qah_tdec_load_layer(self.handle, li, *[_p(a) for a in w16 + w32]))
+
+    def set_rope(self, cos, sin):
+        cos = np.ascontiguousarray(cos, np.float32)
+        sin = np.ascontiguousarray(sin, np.float32)
+        assert cos.shape == sin.shape and cos.shape[1] == self.hd
+        check(host_lib().qah_tdec_set_rope(self.handle, _p(cos), _p(sin), cos.shape[0]))
+
+    def set_attention_flags(self, flags: int):
+        check(host_lib().qah_tdec_set_attention_flags(self.handle, flags))
+
+    def set_hidden(self, h):
+        h = np.ascontiguousarray(h, np.uint16)
+        check(host_lib().qah_tdec_set_hidden(self.handle, h.shape[0], _p(h)))
+
+    def prefill(self, rows):
+        check(host_lib().qah_tdec_prefill(self.handle, rows))
+
+    @property
+    def cap(self) -> int:
+        return (self.max_rows + 63) // 64 * 64
+
+    def read(self, which: str, rows: int) -> np.ndarray:
+        qd, kvd = self.nqh * self.hd, self.nkvh * self.hd
+        idx, shape = {"h": (0, (rows, self.hidden)), "attn": (1, (rows, qd)),
+                      "qkv": (2, (rows, qd + 2 * kvd)), "act": (3, (rows, self.inter)),
+                      "normed": (4, (rows, self.hidden)), "norm2": (5, (rows, self.hidden)),
+                      "q": (6, (self.nqh, rows, self.hd)),
+                      "k_cache": (7, (self.nkvh, self.cap, self.hd)),
+                      "v_cache": (8, (self.nkvh, self.hd, self.cap))}[which]
+        out = np.empty(shape, np.uint16)
+        check(host_lib().qah_tdec_read(self.handle, idx, rows, out.ctypes.data))
+        return out
+
+    def time(self, rows, warmup, steps, use_graph=True) -> tuple[float, float]:
+        """(event ms per step, host wall-clock ms per step)."""
+        ms, wall = ctypes.c_double(), ctypes.c_double()
+        check(host_lib().qah_tdec_time(self.handle, rows, warmup, steps, int(use_graph),
+                                       ctypes.byref(ms), ctypes.byref(wall)))
+        return ms.value, wall.value
+
+    def profile_ops(self, rows, steps) -> dict:
+        out = (ctypes.c_double * 8)()
+        check(host_lib().qah_tdec_profile_ops(self.handle, rows, steps, out))
+        return dict(zip(self.OPS, list(out)))
 
 
 def time_linear(ctx, desc, warmup: int, iters: int) -> float:
