@@ -16,23 +16,27 @@
 //  * S = K . Q^T on v_mfma_f32_32x32x16 (A = 32 keys x 16 d from LDS, B = the
 //    wave's Q fragments, kept in registers for the whole kernel): the lane
 //    holds one query row and 16 of each 32-key tile's scores.
-//  * online softmax in the log2 domain (v_exp_f32): row max / sum over the
-//    lane's values plus its partner lane (lane ^ 32, same row); the running
-//    output is rescaled by exp2(m_old - m_new).
+//  * online softmax in the log2 domain (v_exp_f32): the row max over the
+//    lane's values plus its partner lane (lane ^ 32, same row); the running max
+//    moves only when a block's max exceeds it by more than 2^8, and then the
+//    running output and sum are rescaled by exp2(m_old - m_new); each lane
+//    keeps its half of the row sum until the end.
 //  * O^T += V^T . P^T: P goes from the score registers straight into the
 //    MFMA's B operand.  The reference's GPU path rounds its probabilities to
 //    the 16-bit format before its P.V GEMM (PS = 1 here), which costs up to
 //    2^-11 (f16) / 2^-8 (bf16) relative per weight; by default (PS = 2) the
 //    rounding residue goes through a second MFMA as a second 16-bit term, so
 //    the product carries ~2^-22 / 2^-16 and the result tracks the f32 CPU
-//    path.  f16 probabilities are formed scaled by 2^15 so that none of them
-//    is subnormal (the scale cancels in the final division).  A lane half holds
+//    path.  f16 probabilities are formed scaled by 2^7 so that they stay in
+//    the normal range (the scale cancels in the final division).  A lane half holds
 //    keys {16j+4h..+3, 16j+8+4h..+3} of slice j, so the transposed V cache
 //    stores each aligned group of 16 keys in the order 0-3, 8-11, 4-7, 12-15
 //    (bits 2 and 3 of the key swapped): one 16-byte read per V fragment.
 //  * K and V tiles stream L2 -> LDS with buffer_load ... lds, double-buffered
 //    per split group; chunks are XOR-swizzled per row so the 32-row fragment
 //    reads hit distinct banks.
+#include <type_traits>
+
 #include "qa_internal.h"
 
 namespace qa {
@@ -55,6 +59,25 @@ constexpr int QT = 64;   // query rows per block
 constexpr int KB = 64;   // keys per block
 constexpr int NS = 2;    // key splits per block
 constexpr float kLog2e = 1.44269504088896341f;
+// The running row max is raised only when a block's max exceeds it by more
+// than this (log2 units): probabilities then stay <= 2^kLazy and the output
+// rescale runs once per such jump instead of once per block.
+constexpr float kLazy = 8.f;
+
+// Max / sum of a value over lane pairs (l, l ^ 32), on v_permlane32_swap: the
+// two results hold the wave's lower and upper 32-lane halves exchanged in one
+// of them, so a symmetric combination of both is the pair's result on every
+// lane, identical on the two lanes of a pair.
+__device__ __forceinline__ float pair_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 template <int DT>
 struct AFmt;
@@ -71,9 +94,11 @@ struct AFmt<QA_F16> {
   __device__ static __forceinline__ f32x2 unpack2(uint32_t h) {
     return __builtin_convertvector(__builtin_bit_cast(f16x2, h), f32x2);
   }
-  // Probabilities are formed as p * 2^15 (<= 32768): the f16 range keeps them
-  // normal down to p = 2^-29, so rounding them loses only relative precision.
-  static constexpr float kPBias = 15.f;
+  // Probabilities are formed as p * 2^7; with the running max allowed to lag
+  // the true one by up to 2^8 (kLazy) they stay <= 2^15, and the f16 range
+  // keeps them normal down to p = 2^-21, so rounding them loses only relative
+  // precision (below that, at most 2^-32 absolute).
+  static constexpr float kPBias = 7.f;
 };
 template <>
 struct AFmt<QA_BF16> {
@@ -120,37 +145,46 @@ __global__ void __launch_bounds__(NS * REP * 2 * 64) attention_kernel(const Attn
   constexpr int GW = REP * 2;        // waves per split group
   constexpr int KTILE = KB * HD * 2;  // 16 KB
   constexpr int VTILE = HD * KB * 2;  // 16 KB
-  constexpr int STAGE = KTILE + VTILE;
   constexpr int KI = KB * HD * 2 / 1024 / GW;  // K DMA instructions per wave per block
   constexpr int VI = HD * KB * 2 / 1024 / GW;  // V DMA instructions per wave per block
   constexpr int LPS = KI + VI;
   static_assert(KI * GW * 4 == KB && VI * GW * 8 == HD, "DMA row coverage");
-  __shared__ __attribute__((aligned(1024))) unsigned char smem[NS * 2 * STAGE];
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[NS * 2 * (KTILE + VTILE)];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int split = wave / GW, wg = wave % GW;
   const int hh = wg / 2, rg = wg & 1;
   const int fr = lane & 31, fh = lane >> 5;
 
+  // Block b -> kv head b % nkvh, row tile T - 1 - b / nkvh: the longest key
+  // ranges of every head are dispatched first, and with blocks dealt
+  // round-robin over the 8 XCDs all blocks of a head land on one XCD (for
+  // nkvh a multiple of 8), whose L2 then holds that head's K and V.
   const int T = (int)((p.rows + QT - 1) / QT);
-  const int t = T - 1 - (int)blockIdx.x;  // longest key ranges first
-  const int kvh = blockIdx.y;
+  const int t = T - 1 - (int)(blockIdx.x / p.nkvh);
+  const int kvh = (int)(blockIdx.x % p.nkvh);
   const int head = kvh * REP + hh;
   const int64_t row0 = (int64_t)t * QT;
   const int64_t kend = p.q0 + min(row0 + QT, p.rows);  // keys 0..kend-1 are visible
   const int nkb = (int)((kend + KB - 1) / KB);
-  const int iters = (nkb + NS - 1) / NS;
 
-  // ---- DMA addressing (the group's GW waves share each tile) ----
+  // ---- LDS: per split group, K slots 0/1 then V slots 0/1 (16 KB each) ----
+  unsigned char* gsm = smem + split * 2 * (KTILE + VTILE);
+  auto kslot = [&](int it) { return gsm + (it & 1) * KTILE; };
+  auto vslot = [&](int it) { return gsm + 2 * KTILE + (it & 1) * VTILE; };
+  // this group's steps: key blocks split, split + NS, ... below nkb
+  const int nst = (nkb - split + NS - 1) / NS;
+
+  // ---- DMA (the group's GW waves share each tile) ----
   const uint16_t* kbase = p.k_cache + (int64_t)kvh * p.cap * HD;
   const uint16_t* vbase = p.v_cache + (int64_t)kvh * HD * p.cap;
   const __amdgpu_buffer_rsrc_t rsk = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(kbase), (short)0, (int)(p.cap * HD * 2), 0x00020000);
   const __amdgpu_buffer_rsrc_t rsv = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(vbase), (short)0, (int)(p.cap * HD * 2), 0x00020000);
-  auto issue = [&](int kb, int stage) {
-    unsigned char* sk = smem + (split * 2 + stage) * STAGE;
-    unsigned char* sv = sk + KTILE;
+  auto issue_k = [&](int it) {
+    unsigned char* sk = kslot(it);
+    const int kb = split + NS * it;
 #pragma unroll
     for (int j = 0; j < KI; ++j) {
       const int ins = j * GW + wg;            // 16 instructions, 4 key rows each
@@ -162,6 +196,10 @@ __global__ void __launch_bounds__(NS * REP * 2 * 64) attention_kernel(const Attn
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rsk, (QA_LDS void*)(sk + ins * 1024), 16, off, 0,
                                                0, 0);
     }
+  };
+  auto issue_v = [&](int it) {
+    unsigned char* sv = vslot(it);
+    const int kb = split + NS * it;
 #pragma unroll
     for (int j = 0; j < VI; ++j) {
       const int ins = j * GW + wg;            // 16 instructions, 8 d rows each
@@ -172,6 +210,20 @@ __global__ void __launch_bounds__(NS * REP * 2 * 64) attention_kernel(const Attn
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rsv, (QA_LDS void*)(sv + ins * 1024), 16, off, 0,
                                                0, 0);
     }
+  };
+  // Loads issued by refill(j), in the VALU phase of step j: K(j + 2) into K
+  // slot j & 1 (S(j) has read it) and V(j + 1) into V slot (j + 1) & 1 (P.V of
+  // step j - 1 has read it).  The MFMA phase of step i needs K(i) and V(i - 1),
+  // issued by refill(i - 1); only refill(i)'s loads may still be in flight.
+  auto refill_count = [&](int j) { return (j + 2 < nst ? KI : 0) + (j + 1 < nst ? VI : 0); };
+  auto wait_refill = [&](int c) {
+    static_assert(KI == VI, "refill counts are 0, VI or KI + VI");
+    if (c == LPS)
+      wait_vmcnt<LPS>();
+    else if (c == VI)
+      wait_vmcnt<VI>();
+    else
+      wait_vmcnt<0>();
   };
 
   // ---- this wave's 32 query rows, as MFMA B fragments (8 slices of 16 d) ----
@@ -191,23 +243,56 @@ __global__ void __launch_bounds__(NS * REP * 2 * 64) attention_kernel(const Attn
 #pragma unroll
   for (int i = 0; i < 4; ++i) o[i] = f32x16{0};
   float m_run = -INFINITY, l_run = 0.f;
+  f32x16 s[2] = {f32x16{0}, f32x16{0}};
+  u32x4 pf[4], pl[4];
 
-  auto compute = [&](int kb, int stage) {
-    const unsigned char* sk = smem + (split * 2 + stage) * STAGE;
-    const unsigned char* sv = sk + KTILE;
-    f32x16 s[2] = {f32x16{0}, f32x16{0}};
+  // MFMA phase of step it: P.V of step it - 1 (V slot (it - 1) & 1) and
+  // S = K.Q^T of step it (K slot it & 1), interleaved so that consecutive
+  // MFMAs feed different accumulators.
+  auto mma = [&](auto pv_tag, auto s_tag, int it) {
+    constexpr bool PV = decltype(pv_tag)::value, SQ = decltype(s_tag)::value;
+    const unsigned char* sk = kslot(it);
+    const unsigned char* sv = vslot(it - 1);
+    if constexpr (SQ) {
+      s[0] = f32x16{0};
+      s[1] = f32x16{0};
+    }
 #pragma unroll
-    for (int sl = 0; sl < 8; ++sl) {
+    for (int st = 0; st < 8; ++st) {
+      if constexpr (SQ) {
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-        const int r = kt * 32 + fr;
-        const u32x4 kf =
-            *reinterpret_cast<const u32x4*>(sk + r * 256 + (((2 * sl + fh) ^ kswz(r)) << 4));
-        s[kt] = AFmt<DT>::mfma(kf, qf[sl], s[kt]);
+        for (int kt = 0; kt < 2; ++kt) {
+          const int r = kt * 32 + fr;
+          const u32x4 kf =
+              *reinterpret_cast<const u32x4*>(sk + r * 256 + (((2 * st + fh) ^ kswz(r)) << 4));
+          s[kt] = AFmt<DT>::mfma(kf, qf[st], s[kt]);
+        }
+      }
+      if constexpr (PV) {
+        u32x4 vf[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int q = 2 * st + u, dt = q & 3, j = q >> 2;
+          const int d = dt * 32 + fr;
+          vf[u] = *reinterpret_cast<const u32x4*>(sv + d * 128 + (((2 * j + fh) ^ vswz(d)) << 4));
+          o[dt] = AFmt<DT>::mfma(vf[u], pf[j], o[dt]);
+        }
+        if constexpr (PS == 2) {
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const int q = 2 * st + u, dt = q & 3, j = q >> 2;
+            o[dt] = AFmt<DT>::mfma(vf[u], pl[j], o[dt]);
+          }
+        }
       }
     }
-    // causal mask, only in blocks that cross this wave's diagonal
-    if (kb * KB + KB - 1 > wpos0) {
+  };
+
+  // VALU phase of step it: causal mask, online softmax, P to 16-bit terms,
+  // rescale of O.
+  auto softmax = [&](int it) {
+    const int kb = split + NS * it;
+    if (kb * KB + KB - 1 > wpos0) {  // only blocks that cross this wave's diagonal
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
@@ -216,20 +301,24 @@ __global__ void __launch_bounds__(NS * REP * 2 * 64) attention_kernel(const Attn
           for (int e = 0; e < 4; ++e)
             if (kb * KB + kt * 32 + 8 * g + 4 * fh + e > pos) s[kt][4 * g + e] = -INFINITY;
     }
-    // row max of the raw scores; the scale (> 0) is applied to the max and,
-    // fused, in the exponent: exp2(s sc - m)
-    float bm = -INFINITY;
+    // row max of the raw scores (four independent chains); the scale (> 0)
+    // is applied to the max and, fused, in the exponent: exp2(s sc - m)
+    float mx[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) bm = fmaxf(bm, s[kt][i]);
-    bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
-    const float m_new = fmaxf(m_run, bm * sc);
-    const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-    const float m_b = m_use - AFmt<DT>::kPBias;
-    float rs = 0.f;
-    u32x4 pf[4], pl[4];
+      for (int i = 0; i < 16; ++i) mx[i & 3] = fmaxf(mx[i & 3], s[kt][i]);
+    const float bm = pair_max(fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3]))) * sc;
+    if (__builtin_amdgcn_ballot_w64(bm > m_run + kLazy)) {  // some row's max jumped
+      const float m_new = fmaxf(m_run, bm);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - (m_new == -INFINITY ? 0.f : m_new));
+      l_run *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
+      m_run = m_new;
+    }
+    const float m_b = (m_run == -INFINITY ? 0.f : m_run) - AFmt<DT>::kPBias;
+    float rs[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
@@ -238,7 +327,7 @@ __global__ void __launch_bounds__(NS * REP * 2 * 64) attention_kernel(const Attn
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           pv[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][4 * g + e], sc, -m_b));
-          rs += pv[e];
+          rs[e] += pv[e];
         }
         // slice j = 2 kt + g / 2 holds groups g = 2(j%2), 2(j%2)+1 of tile kt
         const int j = 2 * kt + (g >> 1), half = g & 1;
@@ -251,53 +340,50 @@ __global__ void __launch_bounds__(NS * REP * 2 * 64) attention_kernel(const Attn
           pl[j][2 * half + 1] = AFmt<DT>::pack2(pv[2] - h23[0], pv[3] - h23[1]);
         }
       }
-    rs += __shfl_xor(rs, 32, 64);
-    l_run = l_run * alpha + rs;
-    m_run = m_new;
-    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {  // some row's max moved
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
-    }
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-      const int d = dt * 32 + fr;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const u32x4 vf =
-            *reinterpret_cast<const u32x4*>(sv + d * 128 + (((2 * j + fh) ^ vswz(d)) << 4));
-        o[dt] = AFmt<DT>::mfma(vf, pf[j], o[dt]);
-        if constexpr (PS == 2) o[dt] = AFmt<DT>::mfma(vf, pl[j], o[dt]);
-      }
-    }
+    // this lane's half of the row sum; the halves are added once at the end
+    l_run += (rs[0] + rs[1]) + (rs[2] + rs[3]);
   };
 
-  // ---- main loop: the split groups step through their key blocks in lockstep ----
-  const int kb0 = split;
-  if (kb0 < nkb) issue(kb0, 0);
-  if (kb0 + NS < nkb) issue(kb0 + NS, 1);
-  if (kb0 + NS < nkb)
-    wait_vmcnt<LPS>();
-  else
-    wait_vmcnt<0>();
+  // ---- phases: the two split groups run half a step apart ("ping-pong") ----
+  // A group's step it is an MFMA phase (P.V(it - 1) + S(it)) followed by a
+  // VALU phase (softmax(it)); group 1 runs one phase behind group 0, so on
+  // every SIMD (one wave of each group) one wave's MFMAs overlap the other's
+  // softmax.  Every phase ends in a block barrier, which also orders each
+  // group's LDS reads before the refills that overwrite them.
+  const int n0 = (nkb + 1) / 2, n1 = nkb / 2;
+  const int phases = max(2 * n0 + 1, 2 * n1 + 2);
+  using T_ = std::true_type;
+  using F_ = std::false_type;
+  if (nst > 0) issue_k(0);  // refill(-2)
+  if (nst > 1) issue_k(1);  // refill(-1): K(1), V(0)
+  if (nst > 0) issue_v(0);
+  if (split == 0) wait_refill(refill_count(-1));
   exec_barrier();
-  for (int i = 0; i < iters; ++i) {
-    const int kb = kb0 + NS * i;
-    const int stage = i & 1;
-    if (kb < nkb) compute(kb, stage);
-    wait_lds();
-    exec_barrier();  // every wave is done with this stage's tiles
-    const bool refill = kb + 2 * NS < nkb;
-    if (refill) issue(kb + 2 * NS, stage);
-    if (i + 1 < iters) {
-      if (refill)
-        wait_vmcnt<LPS>();
-      else
-        wait_vmcnt<0>();
-      exec_barrier();  // the next stage has landed for every wave
+  for (int ph = 0; ph < phases; ++ph) {
+    const int my = ph - split;
+    if (my >= 0 && my <= 2 * nst) {
+      const int it = my >> 1;
+      if ((my & 1) == 0) {
+        if (it >= 1 && it < nst)
+          mma(T_{}, T_{}, it);
+        else if (it == 0 && nst > 0)
+          mma(F_{}, T_{}, it);
+        else if (it == nst && it >= 1)
+          mma(T_{}, F_{}, it);
+      } else {
+        if (it + 2 < nst) issue_k(it + 2);
+        if (it + 1 < nst) issue_v(it + 1);
+        softmax(it);
+      }
     }
+    const int nx = ph + 1 - split;  // this wave's next phase
+    if (nx >= 0 && (nx & 1) == 0 && (nx >> 1) <= nst) wait_refill(refill_count((nx >> 1) - 1));
+    wait_lds();
+    exec_barrier();
   }
 
   // ---- merge the two key splits (fixed order) and write the output ----
+  l_run = pair_sum(l_run);  // both lane halves of the row
   __syncthreads();
   float* xch = reinterpret_cast<float*>(smem);  // [GW waves][66 values][64 lanes]
   if (split == 1) {
@@ -336,7 +422,7 @@ __global__ void __launch_bounds__(NS * REP * 2 * 64) attention_kernel(const Attn
 
 hipError_t launch_attention(int dtype, const AttnParams& p, bool p16, hipStream_t s) {
   const int rep = p.nqh / p.nkvh;
-  const dim3 grid((unsigned)((p.rows + QT - 1) / QT), (unsigned)p.nkvh);
+  const dim3 grid((unsigned)((p.rows + QT - 1) / QT * p.nkvh));
   const dim3 block(NS * rep * 2 * 64);
   void (*k)(AttnParams) = nullptr;
 #define QA_ATTN_PICK(R)                                                                      \

@@ -8,7 +8,7 @@ skipped (one rounding of silu(g) * u instead of three).  The mistakes are
 planted in CPU-side results built from the oracle's pieces.
 
 The attention check is pinned the same way: it accepts the GPU kernel's
-arithmetic in both modes (unnormalised probabilities, scaled by 2^15 for f16,
+arithmetic in both modes (unnormalised probabilities, scaled by 2^7 for f16,
 entering the P.V product as two 16-bit terms or rounded once) and the
 reference GPU path's (normalised, then rounded), each emulated here in f64
 with the probabilities rounded as that arithmetic rounds them, and rejects a
@@ -115,11 +115,11 @@ def _attn_emulate(orc, dtype, q, kc, vc, q0, *, mode="split", causal_shift=0,
         if mode == "p16_unscaled":
             o = r16(p / z) @ vf[kh].T
         else:
-            ps = (p * (2.0 ** 15 if dtype == 0 else 1.0)).astype(np.float32)
+            ps = (p * (2.0 ** 7 if dtype == 0 else 1.0)).astype(np.float32)
             pr = r16(ps)
             if mode == "split":
                 pr = pr + r16((ps - pr.astype(np.float32)).astype(np.float64))
-            o = (pr @ vf[kh].T) / (z * (2.0 ** 15 if dtype == 0 else 1.0))
+            o = (pr @ vf[kh].T) / (z * (2.0 ** 7 if dtype == 0 else 1.0))
         out[:, h * hd:(h + 1) * hd] = o
     return orc.h16_from_f32(out.astype(np.float32), dtype)
 
