@@ -246,6 +246,65 @@ typedef struct qa_attention_desc {
 } qa_attention_desc;
 int qa_attention_prefill(qa_ctx* ctx, const qa_attention_desc* desc);
 
+/* ---- audio tower ops around the projections ---- */
+
+/* LayerNorm over each row: y = r16((x - mean) / sqrt(var + eps) * w + b),
+ * mean and variance in f32 from the 16-bit inputs.  Replaces the
+ * `layernorm` dispatches (src/audio_encoder_gpu.rs:1308,1411,1592,1996-2030;
+ * WGSL src/shaders.rs:2680-2754; CPU twin CpuAudioLayerNorm::forward,
+ * src/audio_encoder.rs:147-171).  n a multiple of 8; w, b f32 [n]. */
+typedef struct qa_layer_norm_desc {
+  uint32_t dtype;
+  uint32_t flags; /* reserved, must be 0 */
+  int64_t rows, n;
+  const void* x;
+  int64_t ldx;
+  const float* w;
+  const float* b;
+  void* y;
+  int64_t ldy;
+  float eps;
+} qa_layer_norm_desc;
+int qa_layer_norm(qa_ctx* ctx, const qa_layer_norm_desc* desc);
+
+/* Windowed self-attention of the audio tower: tokens 0..s-1 in windows of
+ * wlen (the last holds the remainder); within a window every token attends
+ * to every token, softmax of q.k / sqrt(hd) in f32.  Head h reads q, k, v at
+ * columns h hd, nh hd + h hd, 2 nh hd + h hd of the fused qkv projection
+ * output [s][ldqkv] and writes out[t][h hd + j].  Replaces the reference's
+ * extract -> win_pack -> scores -> softmax -> av -> attn_flat chain
+ * (src/audio_encoder_gpu.rs:1420-1577; WGSL src/shaders.rs:2756-3086; CPU twin
+ * attention_window, src/audio_encoder.rs:517-616).  hd = 64 and
+ * wlen <= 128 (QA_EUNSUPPORTED otherwise).  The probabilities enter the
+ * P.V product as two 16-bit terms, as in qa_attention_prefill's default. */
+typedef struct qa_window_attention_desc {
+  uint32_t dtype;
+  uint32_t flags; /* reserved, must be 0 */
+  int64_t s;
+  int32_t nh, hd;
+  int64_t wlen;
+  const void* qkv;
+  int64_t ldqkv;
+  void* out;
+  int64_t ldo;
+} qa_window_attention_desc;
+int qa_window_attention(qa_ctx* ctx, const qa_window_attention_desc* desc);
+
+/* y[r][j] = r16(y[r][j] + table[r % period][j]): the sinusoidal position add
+ * after conv_out, row r taking its position within its chunk (`add_pe`,
+ * src/audio_encoder_gpu.rs:1838-1866; WGSL src/shaders.rs:2957-3000; CPU twin src/audio_encoder.rs:331-343).
+ * table f32 [period][n]; n a multiple of 8. */
+typedef struct qa_position_add_desc {
+  uint32_t dtype;
+  uint32_t flags; /* reserved, must be 0 */
+  int64_t rows, n;
+  void* y;
+  int64_t ldy;
+  const float* table;
+  int64_t period;
+} qa_position_add_desc;
+int qa_add_position_table(qa_ctx* ctx, const qa_position_add_desc* desc);
+
 /* Message of the last failure on this thread ("" if none). */
 const char* qa_last_error(void);
 /* Library version string, e.g. "qa 0.1.0 (abi 1, gfx950)". */

@@ -90,6 +90,14 @@ def lib() -> ctypes.CDLL:
         L.or_attention.argtypes = [ci, i64, ci, ci, ci, p, p, p, i64, i64, p, i64]
         L.or_attention.restype = None
         L.or_vperm.argtypes = [i64]
+        L.or_layer_norm.argtypes = [ci, i64, i64, p, i64, p, p, f, p, i64]
+        L.or_layer_norm.restype = None
+        L.or_window_attention.argtypes = [ci, i64, ci, ci, i64, p, i64, p, i64]
+        L.or_window_attention.restype = None
+        L.or_add_position_table.argtypes = [ci, i64, i64, p, i64, p, i64]
+        L.or_add_position_table.restype = None
+        L.or_sinusoid_table.argtypes = [i64, i64, p]
+        L.or_sinusoid_table.restype = None
         L.or_vperm.restype = i64
         L.or_num_threads.restype = ctypes.c_int
         _lib = L
@@ -248,3 +256,38 @@ def attention(dtype: int, q: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarra
     lib().or_attention(dtype, rows, nqh, nkvh, hd, _ptr(q), _ptr(k_cache), _ptr(v_cache), cap,
                        q0, _ptr(out), nqh * hd)
     return out
+
+
+def layer_norm(dtype: int, x: np.ndarray, w: np.ndarray, b: np.ndarray, eps: float) -> np.ndarray:
+    """or_layer_norm: x [rows, n] 16-bit bits, w/b [n] f32 -> [rows, n] bits."""
+    x = _c(x, np.uint16)
+    rows, n = x.shape
+    y = np.empty_like(x)
+    lib().or_layer_norm(dtype, rows, n, _ptr(x), n, _ptr(_c(w, np.float32)),
+                        _ptr(_c(b, np.float32)), ctypes.c_float(eps), _ptr(y), n)
+    return y
+
+
+def window_attention(dtype: int, qkv: np.ndarray, nh: int, hd: int, wlen: int) -> np.ndarray:
+    """or_window_attention: qkv [s, 3*nh*hd] (q | k | v) -> out [s, nh*hd]."""
+    qkv = _c(qkv, np.uint16)
+    s = qkv.shape[0]
+    out = np.empty((s, nh * hd), np.uint16)
+    lib().or_window_attention(dtype, s, nh, hd, wlen, _ptr(qkv), qkv.shape[1], _ptr(out), nh * hd)
+    return out
+
+
+def add_position_table(dtype: int, y: np.ndarray, table: np.ndarray) -> np.ndarray:
+    """or_add_position_table: returns y + table[r % period] (y [rows, n] bits)."""
+    y = _c(y, np.uint16).copy()
+    table = _c(table, np.float32)
+    rows, n = y.shape
+    lib().or_add_position_table(dtype, rows, n, _ptr(y), n, _ptr(table), table.shape[0])
+    return y
+
+
+def sinusoid_table(positions: int, dm: int) -> np.ndarray:
+    """or_sinusoid_table: the audio tower's position table [positions, dm] f32."""
+    t = np.empty((positions, dm), np.float32)
+    lib().or_sinusoid_table(positions, dm, _ptr(t))
+    return t

@@ -112,6 +112,21 @@ void or_attention(int dtype, int64_t rows, int nqh, int nkvh, int hd, const uint
                   const uint16_t* k_cache, const uint16_t* v_cache, int64_t cap, int64_t q0,
                   uint16_t* out, int64_t ldo);
 
+/* ---- audio tower ops around the projections (qa_oracle_audio.c) ----
+ * Parity pins (tests/test_oracle_audio.py): f64 closed forms of LayerNorm
+ * (mean 0 / variance 1 before the affine map, the affine map itself), of
+ * per-window softmax attention (brute force, plus: a window ignores every
+ * other window, identical keys average V, the last window holds the
+ * remainder), the position add (table row r % period), and the sinusoid
+ * table against its definition (sin/cos halves, position 0). */
+void or_layer_norm(int dtype, int64_t rows, int64_t n, const uint16_t* x, int64_t ldx,
+                   const float* w, const float* b, float eps, uint16_t* y, int64_t ldy);
+void or_window_attention(int dtype, int64_t s, int nh, int hd, int64_t wlen, const uint16_t* qkv,
+                         int64_t ldqkv, uint16_t* out, int64_t ldo);
+void or_add_position_table(int dtype, int64_t rows, int64_t n, uint16_t* y, int64_t ldy,
+                           const float* table, int64_t period);
+void or_sinusoid_table(int64_t positions, int64_t dm, float* table);
+
 #ifdef __cplusplus
 }
 #endif

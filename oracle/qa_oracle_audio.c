@@ -1,0 +1,116 @@
+/*
+ * qa_oracle_audio.c -- CPU restatement of the audio tower's non-GEMM ops.
+ *
+ * TEST INFRASTRUCTURE ONLY (see qa_oracle.h): the checker for
+ * qa_layer_norm, qa_window_attention and qa_add_position_table.  Compiled
+ * with -ffp-contract=off so the f32 arithmetic is the CPU path's, operation
+ * for operation.  Inputs and outputs are 16-bit storage (the GPU tower's
+ * buffers); every value is widened to f32 and each output rounded once.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+
+#include "qa_oracle.h"
+
+/* CpuAudioLayerNorm::forward (src/audio_encoder.rs:147-171): mean and
+ * variance by sequential f32 sums, inv_std = 1 / sqrt(var + eps),
+ * y = (x - mean) * inv_std * w + b. */
+void or_layer_norm(int dtype, int64_t rows, int64_t n, const uint16_t* x, int64_t ldx,
+                   const float* w, const float* b, float eps, uint16_t* y, int64_t ldy) {
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < rows; ++r) {
+    const uint16_t* xr = x + r * ldx;
+    float mean = 0.f;
+    for (int64_t j = 0; j < n; ++j) mean += or_h16_to_f32(xr[j], dtype);
+    mean /= (float)n;
+    float var = 0.f;
+    for (int64_t j = 0; j < n; ++j) {
+      const float d = or_h16_to_f32(xr[j], dtype) - mean;
+      var += d * d;
+    }
+    var /= (float)n;
+    const float inv_std = 1.0f / sqrtf(var + eps);
+    for (int64_t j = 0; j < n; ++j) {
+      const float v = (or_h16_to_f32(xr[j], dtype) - mean) * inv_std * w[j] + b[j];
+      y[r * ldy + j] = or_h16_from_f32(v, dtype);
+    }
+  }
+}
+
+/* attention_window (src/audio_encoder.rs:561-616) over every window of
+ * `wlen` tokens (CpuAudioAttention::flat, :517-536: the last window holds the
+ * remainder; a sequence no longer than one window is one window).  Head h
+ * reads q, k, v at columns h*hd, dm + h*hd, 2*dm + h*hd of the fused qkv row
+ * (dm = nh*hd); scores = (q.k, sequential f32 dot) * scale, exp(s - max),
+ * weights = e * (1 / sum), out = sum_k w v accumulated in key order. */
+void or_window_attention(int dtype, int64_t s, int nh, int hd, int64_t wlen, const uint16_t* qkv,
+                         int64_t ldqkv, uint16_t* out, int64_t ldo) {
+  const int64_t dm = (int64_t)nh * hd;
+  const float scale = 1.0f / sqrtf((float)hd);
+  const int64_t nwin = (s + wlen - 1) / wlen;
+#pragma omp parallel for collapse(2) schedule(dynamic)
+  for (int64_t wi = 0; wi < nwin; ++wi)
+    for (int h = 0; h < nh; ++h) {
+      const int64_t st = wi * wlen;
+      const int64_t len = (st + wlen <= s) ? wlen : s - st;
+      float* sc = (float*)malloc((size_t)len * sizeof(float));
+      float* kq = (float*)malloc((size_t)hd * sizeof(float));
+      float* acc = (float*)malloc((size_t)hd * sizeof(float));
+      for (int64_t qi = 0; qi < len; ++qi) {
+        const uint16_t* q = qkv + (st + qi) * ldqkv + (int64_t)h * hd;
+        for (int j = 0; j < hd; ++j) kq[j] = or_h16_to_f32(q[j], dtype);
+        float mx = -INFINITY;
+        for (int64_t ki = 0; ki < len; ++ki) {
+          const uint16_t* k = qkv + (st + ki) * ldqkv + dm + (int64_t)h * hd;
+          float dot = 0.f;
+          for (int j = 0; j < hd; ++j) dot += kq[j] * or_h16_to_f32(k[j], dtype);
+          sc[ki] = dot * scale;
+          if (sc[ki] > mx) mx = sc[ki];
+        }
+        float sum = 0.f;
+        for (int64_t ki = 0; ki < len; ++ki) {
+          sc[ki] = expf(sc[ki] - mx);
+          sum += sc[ki];
+        }
+        const float inv = 1.0f / sum;
+        for (int j = 0; j < hd; ++j) acc[j] = 0.f;
+        for (int64_t ki = 0; ki < len; ++ki) {
+          const float wgt = sc[ki] * inv;
+          const uint16_t* v = qkv + (st + ki) * ldqkv + 2 * dm + (int64_t)h * hd;
+          for (int j = 0; j < hd; ++j) acc[j] += wgt * or_h16_to_f32(v[j], dtype);
+        }
+        uint16_t* o = out + (st + qi) * ldo + (int64_t)h * hd;
+        for (int j = 0; j < hd; ++j) o[j] = or_h16_from_f32(acc[j], dtype);
+      }
+      free(sc);
+      free(kq);
+      free(acc);
+    }
+}
+
+/* The sinusoidal position add after conv_out (CpuConvStem::forward_stages,
+ * src/audio_encoder.rs:331-343; the GPU tower's add_pe): token r gets the
+ * table row r % period (its position within its chunk), y = r16(y + pe). */
+void or_add_position_table(int dtype, int64_t rows, int64_t n, uint16_t* y, int64_t ldy,
+                           const float* table, int64_t period) {
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < rows; ++r) {
+    const float* pe = table + (r % period) * n;
+    for (int64_t j = 0; j < n; ++j)
+      y[r * ldy + j] = or_h16_from_f32(or_h16_to_f32(y[r * ldy + j], dtype) + pe[j], dtype);
+  }
+}
+
+/* CpuConvStem::load (src/audio_encoder.rs:270-283): pe[p][i] = sin(p * e^(-i lt)),
+ * pe[p][half + i] = cos(...), lt = ln(10000) / (half - 1), in f64, stored f32. */
+void or_sinusoid_table(int64_t positions, int64_t dm, float* table) {
+  const int64_t half = dm / 2;
+  const double lt = log(10000.0) / ((double)half - 1.0);
+  for (int64_t p = 0; p < positions; ++p)
+    for (int64_t i = 0; i < half; ++i) {
+      const double a = (double)p * exp(-(double)i * lt);
+      table[p * dm + i] = (float)sin(a);
+      table[p * dm + half + i] = (float)cos(a);
+    }
+}

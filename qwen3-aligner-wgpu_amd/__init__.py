@@ -150,11 +150,62 @@ class AttentionDesc(ctypes.Structure):
     ]
 
 
+class LayerNormDesc(ctypes.Structure):
+    """qa_layer_norm_desc (include/qa.h)."""
+
+    _fields_ = [
+        ("dtype", ctypes.c_uint32),
+        ("flags", ctypes.c_uint32),
+        ("rows", ctypes.c_int64),
+        ("n", ctypes.c_int64),
+        ("x", ctypes.c_void_p),
+        ("ldx", ctypes.c_int64),
+        ("w", ctypes.c_void_p),
+        ("b", ctypes.c_void_p),
+        ("y", ctypes.c_void_p),
+        ("ldy", ctypes.c_int64),
+        ("eps", ctypes.c_float),
+    ]
+
+
+class WindowAttentionDesc(ctypes.Structure):
+    """qa_window_attention_desc (include/qa.h)."""
+
+    _fields_ = [
+        ("dtype", ctypes.c_uint32),
+        ("flags", ctypes.c_uint32),
+        ("s", ctypes.c_int64),
+        ("nh", ctypes.c_int32),
+        ("hd", ctypes.c_int32),
+        ("wlen", ctypes.c_int64),
+        ("qkv", ctypes.c_void_p),
+        ("ldqkv", ctypes.c_int64),
+        ("out", ctypes.c_void_p),
+        ("ldo", ctypes.c_int64),
+    ]
+
+
+class PositionAddDesc(ctypes.Structure):
+    """qa_position_add_desc (include/qa.h)."""
+
+    _fields_ = [
+        ("dtype", ctypes.c_uint32),
+        ("flags", ctypes.c_uint32),
+        ("rows", ctypes.c_int64),
+        ("n", ctypes.c_int64),
+        ("y", ctypes.c_void_p),
+        ("ldy", ctypes.c_int64),
+        ("table", ctypes.c_void_p),
+        ("period", ctypes.c_int64),
+    ]
+
+
 # Every symbol include/qa.h declares (checked by tests/test_abi.py).
 EXPORTS = (
     "qa_ctx_create", "qa_ctx_destroy", "qa_ctx_stream", "qa_alloc", "qa_free",
     "qa_upload", "qa_download", "qa_sync", "qa_linear", "qa_linear_validate",
     "qa_mlp_fused", "qa_rms_norm", "qa_qk_norm_rope", "qa_attention_prefill",
+    "qa_layer_norm", "qa_window_attention", "qa_add_position_table",
     "qa_last_error", "qa_version",
 )
 
@@ -185,6 +236,9 @@ def lib() -> ctypes.CDLL:
         L.qa_rms_norm.argtypes = [vp, ctypes.POINTER(RmsNormDesc)]
         L.qa_qk_norm_rope.argtypes = [vp, ctypes.POINTER(QkRopeDesc)]
         L.qa_attention_prefill.argtypes = [vp, ctypes.POINTER(AttentionDesc)]
+        L.qa_layer_norm.argtypes = [vp, ctypes.POINTER(LayerNormDesc)]
+        L.qa_window_attention.argtypes = [vp, ctypes.POINTER(WindowAttentionDesc)]
+        L.qa_add_position_table.argtypes = [vp, ctypes.POINTER(PositionAddDesc)]
         L.qa_last_error.restype = ctypes.c_char_p
         L.qa_version.restype = ctypes.c_char_p
         for name in EXPORTS:
@@ -295,6 +349,15 @@ class Context:
 
     def attention_prefill(self, desc: AttentionDesc) -> None:
         check(lib().qa_attention_prefill(self.handle, ctypes.byref(desc)))
+
+    def layer_norm(self, desc: LayerNormDesc) -> None:
+        check(lib().qa_layer_norm(self.handle, ctypes.byref(desc)))
+
+    def window_attention(self, desc: WindowAttentionDesc) -> None:
+        check(lib().qa_window_attention(self.handle, ctypes.byref(desc)))
+
+    def add_position_table(self, desc: PositionAddDesc) -> None:
+        check(lib().qa_add_position_table(self.handle, ctypes.byref(desc)))
 
 
 def linear_desc(dtype: int, m: int, n: int, k: int, a, w, c, *, flags: int = 0, bias=None,

@@ -555,4 +555,98 @@ int qa_attention_prefill(qa_ctx* ctx, const qa_attention_desc* d) {
   return e == hipSuccess ? ok() : hip_fail(e, "qa_attention_prefill launch");
 }
 
+int qa_layer_norm(qa_ctx* ctx, const qa_layer_norm_desc* d) {
+  if (!ctx || !d) return fail(QA_EINVAL, "qa_layer_norm: null argument");
+  if (d->dtype != QA_F16 && d->dtype != QA_BF16)
+    return fail(QA_EINVAL, "qa_layer_norm: dtype %u is neither QA_F16 nor QA_BF16", d->dtype);
+  if (d->flags) return fail(QA_EINVAL, "qa_layer_norm: flags must be 0");
+  if (d->rows < 0 || d->n <= 0 || d->n % 8 || d->n > kI32)
+    return fail(QA_EINVAL, "qa_layer_norm: rows >= 0 and n a positive multiple of 8, got %lld x %lld",
+                (long long)d->rows, (long long)d->n);
+  if (d->ldx < d->n || d->ldy < d->n || d->ldx % 8 || d->ldy % 8)
+    return fail(QA_EINVAL, "qa_layer_norm: row strides must be >= n and multiples of 8");
+  if (!d->x || !d->y || !d->w || !d->b) return fail(QA_EINVAL, "qa_layer_norm: null pointer");
+  if (!aligned(d->x, 16) || !aligned(d->y, 16) || !aligned(d->w, 4) || !aligned(d->b, 4))
+    return fail(QA_EINVAL, "qa_layer_norm: x and y must be 16-byte aligned");
+  if (!(d->eps >= 0.0f)) return fail(QA_EINVAL, "qa_layer_norm: eps must be >= 0");
+  if (d->rows == 0) return ok();
+  if (int rc = set_device(ctx)) return rc;
+  qa::LnParams p{};
+  p.x = (const uint16_t*)d->x;
+  p.w = d->w;
+  p.b = d->b;
+  p.y = (uint16_t*)d->y;
+  p.rows = d->rows;
+  p.ldx = d->ldx;
+  p.ldy = d->ldy;
+  p.n = (int)d->n;
+  p.eps = d->eps;
+  const hipError_t e = qa::launch_layer_norm((int)d->dtype, p, ctx->stream);
+  return e == hipSuccess ? ok() : hip_fail(e, "qa_layer_norm launch");
+}
+
+int qa_window_attention(qa_ctx* ctx, const qa_window_attention_desc* d) {
+  if (!ctx || !d) return fail(QA_EINVAL, "qa_window_attention: null argument");
+  if (d->dtype != QA_F16 && d->dtype != QA_BF16)
+    return fail(QA_EINVAL, "qa_window_attention: dtype %u is neither QA_F16 nor QA_BF16",
+                d->dtype);
+  if (d->flags) return fail(QA_EINVAL, "qa_window_attention: flags must be 0");
+  if (d->s < 0 || d->nh <= 0 || d->wlen <= 0)
+    return fail(QA_EINVAL, "qa_window_attention: need s >= 0, nh > 0 and wlen > 0");
+  if (d->hd != 64) return fail(QA_EUNSUPPORTED, "qa_window_attention: hd=%d (only 64)", d->hd);
+  if (d->wlen > 128)
+    return fail(QA_EUNSUPPORTED, "qa_window_attention: wlen=%lld (at most 128)", (long long)d->wlen);
+  const int64_t dm = (int64_t)d->nh * d->hd;
+  if (d->ldqkv < 3 * dm || d->ldqkv % 8 || d->ldo < dm || d->ldo % 8)
+    return fail(QA_EINVAL,
+                "qa_window_attention: ldqkv must be >= 3 nh hd, ldo >= nh hd, both multiples of 8");
+  if ((d->s + d->wlen - 1) / d->wlen * d->nh > kI32)
+    return fail(QA_EINVAL, "qa_window_attention: too many windows");
+  if (!d->qkv || !d->out) return fail(QA_EINVAL, "qa_window_attention: null pointer");
+  if (!aligned(d->qkv, 16) || !aligned(d->out, 16))
+    return fail(QA_EINVAL, "qa_window_attention: qkv and out must be 16-byte aligned");
+  if (d->s == 0) return ok();
+  if (int rc = set_device(ctx)) return rc;
+  qa::WinAttnParams p{};
+  p.qkv = (const uint16_t*)d->qkv;
+  p.out = (uint16_t*)d->out;
+  p.s = d->s;
+  p.wlen = d->wlen;
+  p.ldqkv = d->ldqkv;
+  p.ldo = d->ldo;
+  p.nh = d->nh;
+  p.scale = 1.0f / sqrtf((float)d->hd);
+  const hipError_t e = qa::launch_window_attention((int)d->dtype, p, ctx->stream);
+  return e == hipSuccess ? ok() : hip_fail(e, "qa_window_attention launch");
+}
+
+int qa_add_position_table(qa_ctx* ctx, const qa_position_add_desc* d) {
+  if (!ctx || !d) return fail(QA_EINVAL, "qa_add_position_table: null argument");
+  if (d->dtype != QA_F16 && d->dtype != QA_BF16)
+    return fail(QA_EINVAL, "qa_add_position_table: dtype %u is neither QA_F16 nor QA_BF16",
+                d->dtype);
+  if (d->flags) return fail(QA_EINVAL, "qa_add_position_table: flags must be 0");
+  if (d->rows < 0 || d->n <= 0 || d->n % 8 || d->period <= 0)
+    return fail(QA_EINVAL, "qa_add_position_table: need rows >= 0, n a positive multiple of 8, "
+                           "period > 0");
+  if (d->ldy < d->n || d->ldy % 8)
+    return fail(QA_EINVAL, "qa_add_position_table: ldy must be >= n and a multiple of 8");
+  if (!d->y || !d->table) return fail(QA_EINVAL, "qa_add_position_table: null pointer");
+  if (!aligned(d->y, 16) || !aligned(d->table, 4))
+    return fail(QA_EINVAL, "qa_add_position_table: y must be 16-byte aligned");
+  if (d->rows * (d->n / 8) > kI32 * 256LL)
+    return fail(QA_EINVAL, "qa_add_position_table: too many elements");
+  if (d->rows == 0) return ok();
+  if (int rc = set_device(ctx)) return rc;
+  qa::TableAddParams p{};
+  p.y = (uint16_t*)d->y;
+  p.table = d->table;
+  p.rows = d->rows;
+  p.ldy = d->ldy;
+  p.n = d->n;
+  p.period = d->period;
+  const hipError_t e = qa::launch_add_table((int)d->dtype, p, ctx->stream);
+  return e == hipSuccess ? ok() : hip_fail(e, "qa_add_position_table launch");
+}
+
 }  // extern "C"

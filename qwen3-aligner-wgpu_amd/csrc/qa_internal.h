@@ -102,6 +102,32 @@ struct AttnParams {
   int nqh, nkvh, hd;
   float scale;
 };
+// Audio tower ops (qa_audio_ops.hip).
+struct LnParams {
+  const uint16_t* x;
+  const float* w;
+  const float* b;
+  uint16_t* y;
+  int64_t rows, ldx, ldy;
+  int n;
+  float eps;
+};
+struct TableAddParams {
+  uint16_t* y;
+  const float* table;
+  int64_t rows, ldy, n, period;
+};
+struct WinAttnParams {
+  const uint16_t* qkv;
+  uint16_t* out;
+  int64_t s, wlen, ldqkv, ldo;
+  int nh;
+  float scale;
+};
+hipError_t launch_layer_norm(int dtype, const LnParams& p, hipStream_t stream);
+hipError_t launch_add_table(int dtype, const TableAddParams& p, hipStream_t stream);
+hipError_t launch_window_attention(int dtype, const WinAttnParams& p, hipStream_t stream);
+
 // p16: probabilities rounded once to the 16-bit format (else two 16-bit terms).
 hipError_t launch_attention(int dtype, const AttnParams& p, bool p16, hipStream_t stream);
 

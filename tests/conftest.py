@@ -166,6 +166,27 @@ P_ROUNDING = {
 }
 
 
+def _attention_bound_rows(q, k, v, vis, dtype, mode):
+    """Bound rows [rows, hd] for one head: q [rows, hd], k, v [keys, hd] (f64),
+    vis [rows, keys] the keys each row attends to (see attention_bound)."""
+    hd = q.shape[1]
+    kend = k.shape[0]
+    scale = 1.0 / np.sqrt(hd)
+    u_p, u_abs = P_ROUNDING[mode][dtype]
+    gam = (hd + 16) * 2.0 ** -24
+    acc = (2 * kend + 16) * 2.0 ** -24 + 2.0 ** -20
+    s = q @ k.T * scale
+    sabs = np.abs(q) @ np.abs(k).T * scale
+    s = np.where(vis, s, -np.inf)
+    p = np.exp(s - s.max(axis=1, keepdims=True))
+    z = p.sum(axis=1, keepdims=True)
+    smax = np.where(vis, np.abs(s), 0.0).max(axis=1, keepdims=True)
+    d = gam * np.where(vis, sabs, 0.0).max(axis=1, keepdims=True) + 6 * 2.0 ** -24 * smax
+    va = np.abs(v)
+    wabs = (p @ va) / z
+    return (u_p + np.expm1(2 * d) + acc) * wabs + u_abs * (vis.astype(np.float64) @ va) / z
+
+
 def attention_bound(q_bits, kc_bits, vc_bits, q0, want_bits, orc, dtype, mode="split"):
     """Elementwise bound on |out_gpu - out_ref| for causal GQA attention.
 
@@ -195,25 +216,32 @@ def attention_bound(q_bits, kc_bits, vc_bits, q0, want_bits, orc, dtype, mode="s
     rep = nqh // nkvh
     kend = q0 + rows
     vf = vf[:, :, orc.vperm(cap)[:kend]]  # [nkvh, hd, key]
-    scale = 1.0 / np.sqrt(hd)
-    u_p, u_abs = P_ROUNDING[mode][dtype]
-    gam = (hd + 16) * 2.0 ** -24
-    acc = (2 * kend + 16) * 2.0 ** -24 + 2.0 ** -20
     vis = np.arange(kend)[None, :] <= (q0 + np.arange(rows))[:, None]
     bound = np.zeros((rows, nqh * hd))
     for h in range(nqh):
         kh = h // rep
-        s = q[h] @ kf[kh, :kend].T * scale
-        sabs = np.abs(q[h]) @ np.abs(kf[kh, :kend]).T * scale
-        s = np.where(vis, s, -np.inf)
-        p = np.exp(s - s.max(axis=1, keepdims=True))
-        z = p.sum(axis=1, keepdims=True)
-        smax = np.where(vis, np.abs(s), 0.0).max(axis=1, keepdims=True)
-        d = gam * np.where(vis, sabs, 0.0).max(axis=1, keepdims=True) + 6 * 2.0 ** -24 * smax
-        va = np.abs(vf[kh]).T  # [key, hd]
-        wabs = (p @ va) / z
-        bound[:, h * hd:(h + 1) * hd] = ((u_p + np.expm1(2 * d) + acc) * wabs
-                                         + u_abs * (vis.astype(np.float64) @ va) / z)
+        bound[:, h * hd:(h + 1) * hd] = _attention_bound_rows(q[h], kf[kh, :kend], vf[kh].T, vis,
+                                                              dtype, mode)
+    want = orc.h16_to_f32(want_bits, dtype).astype(np.float64)
+    return bound + ulp16(np.abs(want) + bound, dtype)
+
+
+def window_attention_bound(qkv_bits, nh, hd, wlen, want_bits, orc, dtype, mode="split"):
+    """attention_bound's error model for the audio tower's windowed attention:
+    qkv [s, 3 nh hd] (q | k | v), every token of a window attends to every
+    token of it."""
+    x = orc.h16_to_f32(qkv_bits, dtype).astype(np.float64)
+    s = x.shape[0]
+    dm = nh * hd
+    bound = np.zeros((s, dm))
+    for st in range(0, s, wlen):
+        en = min(s, st + wlen)
+        vis = np.ones((en - st, en - st), bool)
+        for h in range(nh):
+            c = slice(h * hd, (h + 1) * hd)
+            bound[st:en, c] = _attention_bound_rows(
+                x[st:en, c], x[st:en, dm + h * hd:dm + (h + 1) * hd],
+                x[st:en, 2 * dm + h * hd:2 * dm + (h + 1) * hd], vis, dtype, mode)
     want = orc.h16_to_f32(want_bits, dtype).astype(np.float64)
     return bound + ulp16(np.abs(want) + bound, dtype)
 
@@ -228,6 +256,20 @@ def assert_attention(got_bits, want_bits, q_bits, kc_bits, vc_bits, q0, orc, dty
     if mode == "split":
         assert s["max_rel"] <= REL_TOL, s
     bound = attention_bound(q_bits, kc_bits, vc_bits, q0, want_bits, orc, dtype, mode)
+    return _assert_within(got_bits, want_bits, bound, orc, dtype, s)
+
+
+def assert_window_attention(got_bits, want_bits, qkv_bits, nh, hd, wlen, orc, dtype):
+    """Windowed attention against the oracle: finite, the north star (max
+    relative error and MAE) and window_attention_bound elementwise."""
+    s = parity_stats(got_bits, want_bits, orc, dtype)
+    assert s["finite"], s
+    assert s["mae"] <= MAE_TOL and s["max_rel"] <= REL_TOL, s
+    bound = window_attention_bound(qkv_bits, nh, hd, wlen, want_bits, orc, dtype)
+    return _assert_within(got_bits, want_bits, bound, orc, dtype, s)
+
+
+def _assert_within(got_bits, want_bits, bound, orc, dtype, s):
     got = orc.h16_to_f32(got_bits, dtype).astype(np.float64)
     want = orc.h16_to_f32(want_bits, dtype).astype(np.float64)
     excess = np.abs(got - want) - bound

@@ -105,7 +105,10 @@ def test_calls_without_context_fail_cleanly(pkg):
     assert lib.qa_ctx_destroy(None) == pkg.QA_OK
     assert lib.qa_ctx_create(0, None) == pkg.QA_EINVAL
     for fn, desc in ((lib.qa_rms_norm, pkg.RmsNormDesc()), (lib.qa_qk_norm_rope, pkg.QkRopeDesc()),
-                     (lib.qa_attention_prefill, pkg.AttentionDesc())):
+                     (lib.qa_attention_prefill, pkg.AttentionDesc()),
+                     (lib.qa_layer_norm, pkg.LayerNormDesc()),
+                     (lib.qa_window_attention, pkg.WindowAttentionDesc()),
+                     (lib.qa_add_position_table, pkg.PositionAddDesc())):
         assert fn(None, ctypes.byref(desc)) == pkg.QA_EINVAL
         assert "null argument" in pkg.last_error()
 
@@ -119,6 +122,9 @@ def test_decoder_descriptor_layouts(pkg):
         pytest.skip("gcc not available")
     structs = {"qa_rms_norm_desc": pkg.RmsNormDesc, "qa_qk_rope_desc": pkg.QkRopeDesc,
                "qa_attention_desc": pkg.AttentionDesc, "qa_linear_desc": pkg.LinearDesc,
+               "qa_layer_norm_desc": pkg.LayerNormDesc,
+               "qa_window_attention_desc": pkg.WindowAttentionDesc,
+               "qa_position_add_desc": pkg.PositionAddDesc,
                "qa_mlp_desc": pkg.MlpDesc}
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "qa.h"', "int main(void) {"]
     for cname, py in structs.items():

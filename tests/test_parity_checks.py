@@ -157,3 +157,44 @@ def test_attention_check_rejects_mistakes(orc, dtype, mode, mistake):
     bad = _attn_emulate(orc, dtype, q, kc, vc, q0, mode=mode, **kw)
     with pytest.raises(AssertionError):
         assert_attention(bad, want, q, kc, vc, q0, orc, dtype, mode=mode)
+
+
+def _window_emulate(orc, dtype, qkv, nh, hd, wlen, *, shift=0, scale=None):
+    """f64 windowed attention with two-term 16-bit probabilities (the kernel's
+    arithmetic); `shift` moves the window boundaries, `scale` replaces 1/sqrt(hd)."""
+    f = lambda b: orc.h16_to_f32(b, dtype).astype(np.float64)  # noqa: E731
+    r16 = lambda x: f(orc.h16_from_f32(x.astype(np.float32), dtype))  # noqa: E731
+    x = f(qkv)
+    s, dm = x.shape[0], nh * hd
+    scale = 1.0 / np.sqrt(hd) if scale is None else scale
+    out = np.zeros((s, dm))
+    starts = sorted(set([0] + list(range(wlen + shift, s, wlen))))
+    for i, st in enumerate(starts):
+        en = starts[i + 1] if i + 1 < len(starts) else s
+        for h in range(nh):
+            q = x[st:en, h * hd:(h + 1) * hd]
+            k = x[st:en, dm + h * hd:dm + (h + 1) * hd]
+            v = x[st:en, 2 * dm + h * hd:2 * dm + (h + 1) * hd]
+            sc = q @ k.T * scale
+            p = np.exp(sc - sc.max(axis=1, keepdims=True))
+            ps = (p * (2.0 ** 15 if dtype == 0 else 1.0)).astype(np.float32)
+            pr = r16(ps)
+            pr = pr + r16((ps - pr.astype(np.float32)).astype(np.float64))
+            out[st:en, h * hd:(h + 1) * hd] = (pr @ v) / (p.sum(axis=1, keepdims=True)
+                                                          * (2.0 ** 15 if dtype == 0 else 1.0))
+    return orc.h16_from_f32(out.astype(np.float32), dtype)
+
+
+@pytest.mark.parametrize("dtype", [0, 1], ids=["f16", "bf16"])
+def test_window_attention_check_accepts_kernel_and_rejects_mistakes(orc, dtype):
+    from conftest import assert_window_attention
+    rng = np.random.default_rng(11)
+    nh, hd, wlen, s = 2, 64, 24, 70
+    qkv = orc.h16_from_f32((1.5 * rng.standard_normal((s, 3 * nh * hd))).astype(np.float32), dtype)
+    want = orc.window_attention(dtype, qkv, nh, hd, wlen)
+    assert_window_attention(_window_emulate(orc, dtype, qkv, nh, hd, wlen), want, qkv, nh, hd,
+                            wlen, orc, dtype)
+    for kw in (dict(shift=1), dict(scale=1.0)):
+        with pytest.raises(AssertionError):
+            assert_window_attention(_window_emulate(orc, dtype, qkv, nh, hd, wlen, **kw), want,
+                                    qkv, nh, hd, wlen, orc, dtype)
