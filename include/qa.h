@@ -248,6 +248,41 @@ int qa_attention_prefill(qa_ctx* ctx, const qa_attention_desc* desc);
 
 /* ---- audio tower ops around the projections ---- */
 
+/* qa_conv_desc.flags */
+enum {
+  QA_CONV_GELU = 1u << 0,        /* y = gelu(conv + bias), the stem's activation */
+  QA_CONV_TOKEN_MAJOR = 1u << 1  /* output rows ordered (b, wo, ho), not (b, ho, wo) */
+};
+/* One conv level of the audio tower's stem: 3x3 kernel, stride 2, padding 1,
+ * + bias (+ erf GELU), f32 accumulation, one rounding per output.  Replaces
+ * the im2col + gemm_conv + bias_gelu dispatches of a level
+ * (src/audio_encoder_gpu.rs:1165-1201,1714-1794; CPU twin
+ * CpuConvStem::conv_block, src/audio_encoder.rs:204-236,376-447).
+ *   x      [batch][h][w][c_in]  channel-last (the reference keeps [b][c][h][w];
+ *                               channel-last makes each tap's channels one
+ *                               contiguous run, so no im2col is materialised)
+ *   weight [c_out][ldw], ldw = 9 c_in rounded up to 8 (zero-padded):
+ *          k = (kh * 3 + kw) * c_in + ic, i.e. the checkpoint's
+ *          [c_out][c_in][3][3] with c_in moved last
+ *   bias   [c_out] or NULL
+ *   y      [batch * ho * wo][c_out], ho = (h - 1) / 2 + 1, wo = (w - 1) / 2 + 1;
+ *          rows (b, ho, wo), or (b, wo, ho) with QA_CONV_TOKEN_MAJOR -- the
+ *          layout conv_out reads after the last level: row (b, t) then holds
+ *          [f][c], contiguous (the reference's permute,
+ *          src/audio_encoder_gpu.rs:1795-1837, becomes a weight permutation).
+ * c_in = 1 (the mel input) or a multiple of 8 >= 64; c_out a multiple of 8
+ * (<= 1024 when c_in = 1); every operand below 2 GiB. */
+typedef struct qa_conv_desc {
+  uint32_t dtype;
+  uint32_t flags;
+  int64_t batch, h, w, c_in, c_out;
+  const void* x;
+  const void* weight;
+  const void* bias;
+  void* y;
+} qa_conv_desc;
+int qa_conv2d_3x3s2(qa_ctx* ctx, const qa_conv_desc* desc);
+
 /* LayerNorm over each row: y = r16((x - mean) / sqrt(var + eps) * w + b),
  * mean and variance in f32 from the 16-bit inputs.  Replaces the
  * `layernorm` dispatches (src/audio_encoder_gpu.rs:1308,1411,1592,1996-2030;

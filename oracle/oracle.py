@@ -98,6 +98,8 @@ def lib() -> ctypes.CDLL:
         L.or_add_position_table.restype = None
         L.or_sinusoid_table.argtypes = [i64, i64, p]
         L.or_sinusoid_table.restype = None
+        L.or_conv3x3s2.argtypes = [ci, i64, i64, i64, i64, i64, p, p, i64, p, ci, ci, i64, i64, p]
+        L.or_conv3x3s2.restype = None
         L.or_vperm.restype = i64
         L.or_num_threads.restype = ctypes.c_int
         _lib = L
@@ -291,3 +293,21 @@ def sinusoid_table(positions: int, dm: int) -> np.ndarray:
     t = np.empty((positions, dm), np.float32)
     lib().or_sinusoid_table(positions, dm, _ptr(t))
     return t
+
+
+def conv3x3s2(dtype: int, x: np.ndarray, weight: np.ndarray, bias: np.ndarray | None, *,
+              gelu: bool = True, token_major: bool = False, rows: tuple | None = None) -> np.ndarray:
+    """or_conv3x3s2: x [b, h, w, c_in] bits, weight [c_out, ldw] bits (k = (kh*3+kw)*c_in+ic),
+    bias [c_out] bits or None -> y rows [m0, m1) of [b*ho*wo, c_out]."""
+    x = _c(x, np.uint16)
+    weight = _c(weight, np.uint16)
+    b, h, w, c_in = x.shape
+    c_out, ldw = weight.shape
+    ho, wo = (h - 1) // 2 + 1, (w - 1) // 2 + 1
+    m0, m1 = rows if rows is not None else (0, b * ho * wo)
+    y = np.empty((m1 - m0, c_out), np.uint16)
+    bb = _c(bias, np.uint16) if bias is not None else None
+    lib().or_conv3x3s2(dtype, b, h, w, c_in, c_out, _ptr(x), _ptr(weight), ldw,
+                       _ptr(bb) if bb is not None else None, int(gelu), int(token_major), m0, m1,
+                       _ptr(y))
+    return y

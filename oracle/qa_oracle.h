@@ -126,6 +126,12 @@ void or_window_attention(int dtype, int64_t s, int nh, int hd, int64_t wlen, con
 void or_add_position_table(int dtype, int64_t rows, int64_t n, uint16_t* y, int64_t ldy,
                            const float* table, int64_t period);
 void or_sinusoid_table(int64_t positions, int64_t dm, float* table);
+/* Pins (tests/test_oracle_audio.py): torch's float64 conv2d (stride 2,
+ * padding 1) on the same values in NCHW with the checkpoint weight layout,
+ * and a restatement of the reference's im2col + GEMM at small sizes. */
+void or_conv3x3s2(int dtype, int64_t batch, int64_t h, int64_t w, int64_t c_in, int64_t c_out,
+                  const uint16_t* x, const uint16_t* weight, int64_t ldw, const uint16_t* bias,
+                  int gelu, int tmajor, int64_t m0, int64_t m1, uint16_t* y);
 
 #ifdef __cplusplus
 }

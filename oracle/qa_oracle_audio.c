@@ -2,7 +2,8 @@
  * qa_oracle_audio.c -- CPU restatement of the audio tower's non-GEMM ops.
  *
  * TEST INFRASTRUCTURE ONLY (see qa_oracle.h): the checker for
- * qa_layer_norm, qa_window_attention and qa_add_position_table.  Compiled
+ * qa_layer_norm, qa_window_attention, qa_add_position_table and
+ * qa_conv2d_3x3s2.  Compiled
  * with -ffp-contract=off so the f32 arithmetic is the CPU path's, operation
  * for operation.  Inputs and outputs are 16-bit storage (the GPU tower's
  * buffers); every value is widened to f32 and each output rounded once.
@@ -113,4 +114,41 @@ void or_sinusoid_table(int64_t positions, int64_t dm, float* table) {
       table[p * dm + i] = (float)sin(a);
       table[p * dm + half + i] = (float)cos(a);
     }
+}
+
+/* One conv level of the stem on the GPU tower's layouts (qa_conv2d_3x3s2):
+ * 3x3, stride 2, pad 1 (im2col_3x3_s2p1, src/audio_encoder.rs:204-236), the
+ * sum over k = (kh * 3 + kw) * c_in + ic accumulated in f64 (the exact value
+ * the f32 GEMM of conv_block approximates, :376-447), + bias, then the erf
+ * GELU in f32 when `gelu` (:196-202, 439-441) and one rounding.  x is
+ * [batch][h][w][c_in]; weight [c_out][ldw]; rows m0..m1-1 of y [M][c_out],
+ * row order (b, ho, wo), or (b, wo, ho) when `tmajor`. */
+void or_conv3x3s2(int dtype, int64_t batch, int64_t h, int64_t w, int64_t c_in, int64_t c_out,
+                  const uint16_t* x, const uint16_t* weight, int64_t ldw, const uint16_t* bias,
+                  int gelu, int tmajor, int64_t m0, int64_t m1, uint16_t* y) {
+  const int64_t ho = (h - 1) / 2 + 1, wo = (w - 1) / 2 + 1, plane = ho * wo;
+  (void)batch;
+#pragma omp parallel for schedule(dynamic, 4)
+  for (int64_t m = m0; m < m1; ++m) {
+    const int64_t b = m / plane, q = m % plane;
+    const int64_t oh = tmajor ? q % ho : q / wo;
+    const int64_t ow = tmajor ? q / ho : q % wo;
+    for (int64_t oc = 0; oc < c_out; ++oc) {
+      const uint16_t* wr = weight + oc * ldw;
+      double acc = 0.0;
+      for (int kh = 0; kh < 3; ++kh)
+        for (int kw = 0; kw < 3; ++kw) {
+          const int64_t ih = 2 * oh + kh - 1, iw = 2 * ow + kw - 1;
+          if (ih < 0 || ih >= h || iw < 0 || iw >= w) continue;
+          const uint16_t* xp = x + ((b * h + ih) * w + iw) * c_in;
+          const uint16_t* wp = wr + (kh * 3 + kw) * c_in;
+          for (int64_t ic = 0; ic < c_in; ++ic)
+            acc += (double)or_h16_to_f32(xp[ic], dtype) * (double)or_h16_to_f32(wp[ic], dtype);
+        }
+      if (bias) acc += (double)or_h16_to_f32(bias[oc], dtype);
+      float v = (float)acc;
+      if (gelu) v = or_gelu(v);
+      y[(m - m0) * c_out + oc] = or_h16_from_f32(v, dtype);
+    }
+  }
 }

@@ -29,6 +29,7 @@ QA_OK, QA_EINVAL, QA_ENOMEM, QA_EDEVICE, QA_EUNSUPPORTED = 0, -1, -2, -3, -4
 F16, BF16 = 0, 1
 ACCUMULATE, EPI_GELU, EPI_SILU_MUL, TRANSB, BIAS_ROWS = 1, 2, 4, 8, 16
 QA_ATTN_P16 = 1  # qa_attention_desc.flags
+QA_CONV_GELU, QA_CONV_TOKEN_MAJOR = 1, 2  # qa_conv_desc.flags
 
 _STATUS = {
     QA_EINVAL: "QA_EINVAL",
@@ -200,12 +201,30 @@ class PositionAddDesc(ctypes.Structure):
     ]
 
 
+class ConvDesc(ctypes.Structure):
+    """qa_conv_desc (include/qa.h)."""
+
+    _fields_ = [
+        ("dtype", ctypes.c_uint32),
+        ("flags", ctypes.c_uint32),
+        ("batch", ctypes.c_int64),
+        ("h", ctypes.c_int64),
+        ("w", ctypes.c_int64),
+        ("c_in", ctypes.c_int64),
+        ("c_out", ctypes.c_int64),
+        ("x", ctypes.c_void_p),
+        ("weight", ctypes.c_void_p),
+        ("bias", ctypes.c_void_p),
+        ("y", ctypes.c_void_p),
+    ]
+
+
 # Every symbol include/qa.h declares (checked by tests/test_abi.py).
 EXPORTS = (
     "qa_ctx_create", "qa_ctx_destroy", "qa_ctx_stream", "qa_alloc", "qa_free",
     "qa_upload", "qa_download", "qa_sync", "qa_linear", "qa_linear_validate",
     "qa_mlp_fused", "qa_rms_norm", "qa_qk_norm_rope", "qa_attention_prefill",
-    "qa_layer_norm", "qa_window_attention", "qa_add_position_table",
+    "qa_layer_norm", "qa_window_attention", "qa_add_position_table", "qa_conv2d_3x3s2",
     "qa_last_error", "qa_version",
 )
 
@@ -239,6 +258,7 @@ def lib() -> ctypes.CDLL:
         L.qa_layer_norm.argtypes = [vp, ctypes.POINTER(LayerNormDesc)]
         L.qa_window_attention.argtypes = [vp, ctypes.POINTER(WindowAttentionDesc)]
         L.qa_add_position_table.argtypes = [vp, ctypes.POINTER(PositionAddDesc)]
+        L.qa_conv2d_3x3s2.argtypes = [vp, ctypes.POINTER(ConvDesc)]
         L.qa_last_error.restype = ctypes.c_char_p
         L.qa_version.restype = ctypes.c_char_p
         for name in EXPORTS:
@@ -358,6 +378,9 @@ class Context:
 
     def add_position_table(self, desc: PositionAddDesc) -> None:
         check(lib().qa_add_position_table(self.handle, ctypes.byref(desc)))
+
+    def conv2d_3x3s2(self, desc: ConvDesc) -> None:
+        check(lib().qa_conv2d_3x3s2(self.handle, ctypes.byref(desc)))
 
 
 def linear_desc(dtype: int, m: int, n: int, k: int, a, w, c, *, flags: int = 0, bias=None,

@@ -149,6 +149,8 @@ constexpr double kReduceGBs = 3000.0;   // split-K reduce kernel, partials from 
 // Tile / split-K choice: the modelled time of each candidate is
 // rounds x (fixed + stages x stage_us) (+ the reduce kernel when K is split),
 // where rounds = ceil(units / CUs); the cheapest candidate wins.
+void choose_group_m(qa::Plan& pl);
+
 qa::Plan plan_linear(const qa_linear_desc& d, int num_cus) {
   qa::Plan pl{};
   const bool silu = d.flags & QA_EPI_SILU_MUL;
@@ -197,12 +199,16 @@ qa::Plan plan_linear(const qa_linear_desc& d, int num_cus) {
     }
   }
   if (pl.splits > 1) pl.ws_floats = (size_t)pl.splits * (size_t)M * (size_t)N;
+  choose_group_m(pl);
+  return pl;
+}
 
-  // Tile enumeration bands (tile_of): each XCD takes a contiguous range of
-  // about per = tiles/8 tiles, which with bands of g m-tiles covers g m-tiles
-  // x ceil(per/g) n-tiles; its L2 fetches those A rows (bm each) and W rows
-  // (bn each, both halves of a SiLU tile).  The cheapest g wins, the whole
-  // n-column order (g = tiles_m) on ties.  QA_GROUP_M forces g.
+// Tile enumeration bands (tile_of): each XCD takes a contiguous range of
+// about per = tiles/8 tiles, which with bands of g m-tiles covers g m-tiles
+// x ceil(per/g) n-tiles; its L2 fetches those A rows (bm each) and W rows
+// (bn each, both halves of a SiLU tile).  The cheapest g wins, the whole
+// n-column order (g = tiles_m) on ties.  QA_GROUP_M forces g.
+void choose_group_m(qa::Plan& pl) {
   {
     const qa::TileShape ts = qa::tile_shape(pl.tile);
     const int64_t tm = pl.tiles_m, tn = pl.tiles_n;
@@ -224,6 +230,38 @@ qa::Plan plan_linear(const qa_linear_desc& d, int num_cus) {
       if (g >= 1) pl.group_m = (int)std::min<int64_t>(g, tm);
     }
   }
+}
+
+// The implicit-GEMM convolution: M = output pixels, N = c_out, K = 9 c_in,
+// never split (K is long), on the tile shapes the CV loader is built for.
+qa::Plan plan_conv(int64_t M, int64_t N, int64_t K, bool gelu, int num_cus) {
+  qa::Plan pl{};
+  pl.epi = gelu ? qa::EPI_GELU : qa::EPI_PLAIN;
+  pl.conv = true;
+  pl.splits = 1;
+  pl.kchunk = (int)((K + 63) / 64 * 64);
+  double best = 1e300;
+  int forced_tile = -1;
+  if (const char* e = getenv("QA_TILE")) forced_tile = atoi(e);
+  for (const int tile : {qa::TILE_128x128, qa::TILE_256x128}) {
+    if (forced_tile >= 0 && forced_tile != tile) continue;
+    const qa::TileShape ts = qa::tile_shape(tile);
+    const int64_t tm = (M + ts.bm - 1) / ts.bm, tn = (N + ts.bn - 1) / ts.bn;
+    const int64_t rounds = (tm * tn + num_cus - 1) / num_cus;
+    const double cost = (double)rounds * (kTileFixedUs + (double)pl.kchunk / 64.0 * stage_us(tile));
+    if (cost < best * 0.999) {
+      best = cost;
+      pl.tile = tile;
+      pl.tiles_m = (int)tm;
+      pl.tiles_n = (int)tn;
+    }
+  }
+  if (best == 1e300) {  // a forced tile the conv path does not have
+    pl.tile = qa::TILE_128x128;
+    pl.tiles_m = (int)((M + 127) / 128);
+    pl.tiles_n = (int)((N + 127) / 128);
+  }
+  choose_group_m(pl);
   return pl;
 }
 
@@ -553,6 +591,83 @@ int qa_attention_prefill(qa_ctx* ctx, const qa_attention_desc* d) {
   p.scale = 1.0f / sqrtf((float)d->hd);
   const hipError_t e = qa::launch_attention((int)d->dtype, p, (d->flags & QA_ATTN_P16) != 0, ctx->stream);
   return e == hipSuccess ? ok() : hip_fail(e, "qa_attention_prefill launch");
+}
+
+int qa_conv2d_3x3s2(qa_ctx* ctx, const qa_conv_desc* d) {
+  if (!ctx || !d) return fail(QA_EINVAL, "qa_conv2d_3x3s2: null argument");
+  if (d->dtype != QA_F16 && d->dtype != QA_BF16)
+    return fail(QA_EINVAL, "qa_conv2d_3x3s2: dtype %u is neither QA_F16 nor QA_BF16", d->dtype);
+  if (d->flags & ~(uint32_t)(QA_CONV_GELU | QA_CONV_TOKEN_MAJOR))
+    return fail(QA_EINVAL, "qa_conv2d_3x3s2: unknown flags 0x%x",
+                d->flags & ~(uint32_t)(QA_CONV_GELU | QA_CONV_TOKEN_MAJOR));
+  if (d->batch < 0 || d->h <= 0 || d->w <= 0 || d->c_in <= 0 || d->c_out <= 0)
+    return fail(QA_EINVAL, "qa_conv2d_3x3s2: bad shape");
+  if (d->c_out % 8) return fail(QA_EINVAL, "qa_conv2d_3x3s2: c_out must be a multiple of 8");
+  const bool direct = d->c_in == 1;
+  if (!direct && (d->c_in % 8 || d->c_in < 64))
+    return fail(QA_EUNSUPPORTED,
+                "qa_conv2d_3x3s2: c_in=%lld (1, or a multiple of 8 >= 64)", (long long)d->c_in);
+  if (direct && d->c_out > 1024)
+    return fail(QA_EUNSUPPORTED, "qa_conv2d_3x3s2: c_out=%lld > 1024 with c_in = 1",
+                (long long)d->c_out);
+  const int64_t ho = (d->h - 1) / 2 + 1, wo = (d->w - 1) / 2 + 1;
+  const int64_t M = d->batch * ho * wo;
+  const int64_t K = 9 * d->c_in, ldw = (K + 7) / 8 * 8;
+  if (d->batch * d->h * d->w * d->c_in * 2 > kI32 || M * d->c_out > kI32 * 4LL ||
+      d->c_out * ldw * 2 > kI32 || M > kI32)
+    return fail(QA_EINVAL, "qa_conv2d_3x3s2: operands must stay below 2 GiB");
+  if (!d->x || !d->weight || !d->y) return fail(QA_EINVAL, "qa_conv2d_3x3s2: null pointer");
+  if (!aligned(d->x, 16) || !aligned(d->weight, 16) || !aligned(d->y, 16) ||
+      (d->bias && !aligned(d->bias, 8)))
+    return fail(QA_EINVAL, "qa_conv2d_3x3s2: x, weight and y must be 16-byte aligned, bias 8");
+  if (M == 0) return ok();
+  if (int rc = set_device(ctx)) return rc;
+  const bool gelu = (d->flags & QA_CONV_GELU) != 0, tmajor = (d->flags & QA_CONV_TOKEN_MAJOR) != 0;
+  if (direct) {
+    qa::Conv1Params p{};
+    p.x = (const uint16_t*)d->x;
+    p.w = (const uint16_t*)d->weight;
+    p.bias = (const uint16_t*)d->bias;
+    p.y = (uint16_t*)d->y;
+    p.M = M;
+    p.h = (int)d->h;
+    p.w_in = (int)d->w;
+    p.ho = (int)ho;
+    p.wo = (int)wo;
+    p.c_out = (int)d->c_out;
+    p.ldw = (int)ldw;
+    p.tmajor = tmajor;
+    p.gelu = gelu;
+    const hipError_t e = qa::launch_conv1((int)d->dtype, p, ctx->stream);
+    return e == hipSuccess ? ok() : hip_fail(e, "qa_conv2d_3x3s2 launch");
+  }
+  const qa::Plan plan = plan_conv(M, d->c_out, K, gelu, ctx->num_cus);
+  qa::GemmParams p{};
+  p.a = (const uint16_t*)d->x;
+  p.w = (const uint16_t*)d->weight;
+  p.c = (uint16_t*)d->y;
+  p.bias = (const uint16_t*)d->bias;
+  p.a_bytes = (int)(d->batch * d->h * d->w * d->c_in * 2);
+  p.w_bytes = (int)(d->c_out * ldw * 2);
+  p.M = (int)M;
+  p.N = (int)d->c_out;
+  p.K = (int)K;
+  p.lda = (int)K;
+  p.ldb = (int)ldw;
+  p.ldc = (int)d->c_out;
+  p.tiles_m = plan.tiles_m;
+  p.tiles_n = plan.tiles_n;
+  p.splits = 1;
+  p.kchunk = plan.kchunk;
+  p.group_m = plan.group_m;
+  p.cv_c = (int)d->c_in;
+  p.cv_h = (int)d->h;
+  p.cv_w = (int)d->w;
+  p.cv_ho = (int)ho;
+  p.cv_wo = (int)wo;
+  p.cv_tmajor = tmajor;
+  const hipError_t e = qa::launch_gemm((int)d->dtype, plan, p, 1, ctx->stream);
+  return e == hipSuccess ? ok() : hip_fail(e, "qa_conv2d_3x3s2 launch");
 }
 
 int qa_layer_norm(qa_ctx* ctx, const qa_layer_norm_desc* d) {

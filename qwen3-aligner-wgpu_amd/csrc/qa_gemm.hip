@@ -160,22 +160,8 @@ __device__ __forceinline__ void exec_barrier() {
 // ulps, far below the 16-bit rounding that follows.
 constexpr float kLog2e = 1.44269504088896341f;
 
-// erf GELU, 0.5 x (1 + erf(x / sqrt 2)) (src/audio_encoder.rs:196-202), with
-// erf from Abramowitz & Stegun 7.1.26 (|error| <= 1.5e-7; the reference's GPU
-// path uses the same approximation, src/shaders.rs:2593-2625):
-//   erf(a) = 1 - P(t) e^{-a^2},  t = 1 / (1 + 0.3275911 a),  a >= 0.
-// For x < 0 the factor 1 + erf(x / sqrt 2) = P(t) e^{-a^2} is formed directly,
-// without cancelling against 1.
-__device__ __forceinline__ float gelu_erf(float x) {
-  const float a = fabsf(x) * 0.70710678118654752f;
-  const float t = __builtin_amdgcn_rcpf(1.0f + 0.3275911f * a);
-  const float poly =
-      ((((1.061405429f * t - 1.453152027f) * t + 1.421413741f) * t - 0.284496736f) * t +
-       0.254829592f) * t;
-  const float q = poly * __builtin_amdgcn_exp2f(-a * a * kLog2e);  // 1 - erf(a)
-  return 0.5f * x * (x >= 0.0f ? 2.0f - q : q);
-}
-
+// The erf GELU is gelu_erf (qa_internal.h).
+//
 // g * sigmoid(g) * u with sigmoid(g) = 1 / (1 + 2^(-g log2 e)), the reference
 // GPU kernel's form (src/shaders.rs:1411-1450).
 __device__ __forceinline__ float silu_mul(float g, float u) {
@@ -346,7 +332,15 @@ __device__ __forceinline__ void finish_tile(const GemmParams& p, f32x16 (&acc)[F
 // waves issue the DMA themselves; with PW > 0, PW producer waves (after the
 // MMA waves) issue all of it and only take part in the barriers and the
 // epilogue.
-template <int DT, int BM, int BN, int S, int EPI, int KG, int PW>
+//
+// With CV = 1 the A operand is implicit: row m is an output pixel of a 3x3,
+// stride-2, pad-1 convolution over a channel-last input [b][H][W][C], and
+// k = (kh * 3 + kw) * C + ic, so every 16-byte chunk of the row is 8
+// consecutive input channels of one tap (C a multiple of 8): the DMA address
+// is computed per chunk, and taps in the zero padding read as zeros through
+// the buffer resource's range check (the im2col of src/audio_encoder.rs:
+// 204-236, never materialised).
+template <int DT, int BM, int BN, int S, int EPI, int KG, int PW, int CV = 0>
 __global__ void __launch_bounds__(NT * KG + 64 * PW) gemm_dma_kernel(const GemmParams p) {
   constexpr int NMW = 4 * KG;                // MMA waves
   constexpr int NTH = NT * KG + 64 * PW;     // threads
@@ -399,12 +393,21 @@ __global__ void __launch_bounds__(NT * KG + 64 * PW) gemm_dma_kernel(const GemmP
   const int lrow = lane >> 3, pchunk = lane & 7;
   uint32_t aoff[AJ], woff[BJ];
   int akc[AJ], wkc[BJ];  // k offset (elements) of the fetched chunk
+  int cpix[AJ], cih[AJ], ciw[AJ];  // CV: image's first pixel, input row / column of tap (0, 0)
 #pragma unroll
   for (int j = 0; j < AJ; ++j) {
     const int r = (j * NW + dwave) * 8 + lrow;
     const int m = m0 + r;
     akc[j] = (pchunk ^ swz(r)) * 8;
     aoff[j] = m < p.M ? (uint32_t)(((int64_t)m * p.lda + akc[j]) * 2) : OOB;
+    if constexpr (CV) {
+      const int plane = p.cv_ho * p.cv_wo, b = m / plane, q = m - b * plane;
+      const int ho = p.cv_tmajor ? q % p.cv_ho : q / p.cv_wo;
+      const int wo = p.cv_tmajor ? q / p.cv_ho : q % p.cv_wo;
+      cpix[j] = b * p.cv_h * p.cv_w;
+      cih[j] = m < p.M ? 2 * ho - 1 : INT32_MIN / 2;  // rows >= M never in range
+      ciw[j] = 2 * wo - 1;
+    }
   }
 #pragma unroll
   for (int j = 0; j < BJ; ++j) {
@@ -419,8 +422,18 @@ __global__ void __launch_bounds__(NT * KG + 64 * PW) gemm_dma_kernel(const GemmP
     unsigned char* sb = smem + buf * STAGE;
 #pragma unroll
     for (int j = 0; j < AJ; ++j) {
-      const bool ok = k0 + akc[j] < kend && aoff[j] != OOB;
-      const uint32_t off = ok ? aoff[j] + (uint32_t)k0 * 2u : OOB;
+      uint32_t off;
+      if constexpr (CV) {
+        const int k = k0 + akc[j];
+        const int g = k / p.cv_c, ic = k - g * p.cv_c;  // tap g = 3 kh + kw
+        const int kh = (g * 11) >> 5, kw = g - 3 * kh;   // g / 3 for g < 9
+        const int ih = cih[j] + kh, iw = ciw[j] + kw;
+        const bool ok = k < kend && (unsigned)ih < (unsigned)p.cv_h && (unsigned)iw < (unsigned)p.cv_w;
+        off = ok ? (uint32_t)(((cpix[j] + ih * p.cv_w + iw) * p.cv_c + ic) * 2) : OOB;
+      } else {
+        const bool ok = k0 + akc[j] < kend && aoff[j] != OOB;
+        off = ok ? aoff[j] + (uint32_t)k0 * 2u : OOB;
+      }
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (QA_LDS void*)(sb + (j * NW + dwave) * 1024),
                                                16, off, 0, 0, 0);
     }
@@ -736,11 +749,11 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(const GemmParams p) 
   epilogue4<DT, EPI>(p, p.c, m, n, v, uu);
 }
 
-template <int DT, int BM, int BN, int S, int EPI, int KG, int PW>
+template <int DT, int BM, int BN, int S, int EPI, int KG, int PW, int CV = 0>
 hipError_t launch_dma(const Plan& plan, const GemmParams& p, int batch, hipStream_t s) {
   const unsigned units = (unsigned)(plan.tiles_m * plan.tiles_n * plan.splits);
-  hipLaunchKernelGGL((gemm_dma_kernel<DT, BM, BN, S, EPI, KG, PW>), dim3(units, (unsigned)batch),
-                     dim3(NT * KG + 64 * PW), 0, s, p);
+  hipLaunchKernelGGL((gemm_dma_kernel<DT, BM, BN, S, EPI, KG, PW, CV>),
+                     dim3(units, (unsigned)batch), dim3(NT * KG + 64 * PW), 0, s, p);
   return hipGetLastError();
 }
 
@@ -763,7 +776,13 @@ hipError_t launch_reduce(const GemmParams& p, hipStream_t s) {
 template <int DT, int EPI>
 hipError_t launch_epi(const Plan& plan, const GemmParams& p, int batch, hipStream_t s) {
   hipError_t e;
-  if (plan.transb) {
+  if (plan.conv) {  // implicit-GEMM convolution (qa_conv2d_3x3s2)
+    if constexpr (EPI == EPI_SILU) return hipErrorInvalidValue;  // never planned
+    else if (plan.tile == TILE_256x128)
+      e = launch_dma<DT, 256, 128, 3, EPI, 2, 0, 1>(plan, p, batch, s);
+    else
+      e = launch_dma<DT, 128, 128, 5, EPI, 2, 8, 1>(plan, p, batch, s);
+  } else if (plan.transb) {
     if constexpr (EPI == EPI_SILU) return hipErrorInvalidValue;  // rejected by validation
     else e = launch_reg<DT, EPI>(plan, p, batch, s);
   } else {

@@ -41,6 +41,23 @@ inline TileShape tile_shape(int cfg) {
 }
 
 // Kernel parameters (passed by value).  Element units throughout.
+// erf-form GELU, 0.5 x (1 + erf(x / sqrt 2)), with erf from Abramowitz &
+// Stegun 7.1.26 (|error| <= 1.5e-7) on v_exp_f32 / v_rcp_f32: the form of the
+// reference's `audio_bias_gelu` (src/shaders.rs:2593-2625); the CPU twin calls
+// libm's erff (src/audio_encoder.rs:196-202).
+//   erf(a) = 1 - P(t) e^{-a^2},  t = 1 / (1 + 0.3275911 a),  a >= 0;
+// for x < 0 the factor 1 + erf(x / sqrt 2) = P(t) e^{-a^2} is formed directly,
+// without cancelling against 1.
+__device__ __forceinline__ float gelu_erf(float x) {
+  const float a = fabsf(x) * 0.70710678118654752f;
+  const float t = __builtin_amdgcn_rcpf(1.0f + 0.3275911f * a);
+  const float poly =
+      ((((1.061405429f * t - 1.453152027f) * t + 1.421413741f) * t - 0.284496736f) * t +
+       0.254829592f) * t;
+  const float q = poly * __builtin_amdgcn_exp2f(-a * a * 1.44269504088896341f);  // 1 - erf(a)
+  return 0.5f * x * (x >= 0.0f ? 2.0f - q : q);
+}
+
 struct GemmParams {
   const uint16_t* a;
   const uint16_t* w;
@@ -57,6 +74,10 @@ struct GemmParams {
   int accumulate;        // add C_old before the rounding
   int bias_rows;         // bias indexed by output row (channel-major conv)
   int group_m;           // m-tiles per band of the tile enumeration (tile_of)
+  // implicit 3x3 / stride-2 / pad-1 convolution A operand (Plan::conv)
+  int cv_c, cv_h, cv_w;  // input channels (multiple of 8, >= 64), height, width
+  int cv_ho, cv_wo;      // output height, width
+  int cv_tmajor;         // output rows ordered (b, wo, ho) instead of (b, ho, wo)
 };
 
 struct Plan {
@@ -66,6 +87,7 @@ struct Plan {
   int tiles_m, tiles_n, splits, kchunk;
   int group_m;        // see GemmParams::group_m
   size_t ws_floats;   // split-K partial floats needed
+  bool conv = false;  // A is an implicit convolution operand (GemmParams::cv_*)
 };
 
 // Launch one planned GEMM on `stream` (grid = tiles*splits x batch).
@@ -127,6 +149,19 @@ struct WinAttnParams {
 hipError_t launch_layer_norm(int dtype, const LnParams& p, hipStream_t stream);
 hipError_t launch_add_table(int dtype, const TableAddParams& p, hipStream_t stream);
 hipError_t launch_window_attention(int dtype, const WinAttnParams& p, hipStream_t stream);
+
+// Direct 3x3 / stride-2 / pad-1 convolution of a single-channel input
+// (qa_conv.hip): the first conv level, where the implicit GEMM's 8-channel
+// chunks do not apply.
+struct Conv1Params {
+  const uint16_t* x;     // [b][h][w]
+  const uint16_t* w;     // [c_out][ldw], taps kh * 3 + kw
+  const uint16_t* bias;  // [c_out] or nullptr
+  uint16_t* y;           // [M][c_out]
+  int64_t M;
+  int h, w_in, ho, wo, c_out, ldw, tmajor, gelu;
+};
+hipError_t launch_conv1(int dtype, const Conv1Params& p, hipStream_t stream);
 
 // p16: probabilities rounded once to the 16-bit format (else two 16-bit terms).
 hipError_t launch_attention(int dtype, const AttnParams& p, bool p16, hipStream_t stream);

@@ -108,7 +108,8 @@ def test_calls_without_context_fail_cleanly(pkg):
                      (lib.qa_attention_prefill, pkg.AttentionDesc()),
                      (lib.qa_layer_norm, pkg.LayerNormDesc()),
                      (lib.qa_window_attention, pkg.WindowAttentionDesc()),
-                     (lib.qa_add_position_table, pkg.PositionAddDesc())):
+                     (lib.qa_add_position_table, pkg.PositionAddDesc()),
+                     (lib.qa_conv2d_3x3s2, pkg.ConvDesc())):
         assert fn(None, ctypes.byref(desc)) == pkg.QA_EINVAL
         assert "null argument" in pkg.last_error()
 
@@ -124,7 +125,7 @@ def test_decoder_descriptor_layouts(pkg):
                "qa_attention_desc": pkg.AttentionDesc, "qa_linear_desc": pkg.LinearDesc,
                "qa_layer_norm_desc": pkg.LayerNormDesc,
                "qa_window_attention_desc": pkg.WindowAttentionDesc,
-               "qa_position_add_desc": pkg.PositionAddDesc,
+               "qa_position_add_desc": pkg.PositionAddDesc, "qa_conv_desc": pkg.ConvDesc,
                "qa_mlp_desc": pkg.MlpDesc}
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "qa.h"', "int main(void) {"]
     for cname, py in structs.items():

@@ -1,6 +1,6 @@
 """Pins the audio-tower op restatements in oracle/qa_oracle_audio.c before they
 are trusted as the checker for qa_layer_norm / qa_window_attention /
-qa_add_position_table.
+qa_add_position_table / qa_conv2d_3x3s2.
 
 The reference ships no known-answer vectors for these ops, so each is checked
 against what the mathematics fixes:
@@ -15,8 +15,13 @@ against what the mathematics fixes:
     rounding; row r takes table row r % period.
   * the sinusoid table (src/audio_encoder.rs:270-283): its definition in f64,
     position 0 = [0 ... 0 | 1 ... 1].
+  * the conv level (src/audio_encoder.rs:204-236,376-447): torch's float64
+    conv2d (stride 2, padding 1, NCHW, the checkpoint's weight layout) plus
+    GELU, and a restatement of the reference's own im2col times its weight
+    matrix; both output row orders.
 A dropped mean, a variance without the square, a missing 1/sqrt(hd), a window
-boundary off by one or a table row off by one fails one of them.
+boundary off by one, a table row off by one, a transposed tap, a wrong stride
+or padding fails one of them.
 """
 from __future__ import annotations
 
@@ -136,3 +141,61 @@ def test_sinusoid_table_definition(orc):
     ang = np.arange(pos)[:, None] * inv[None, :]
     assert np.abs(t[:, :half] - np.sin(ang)).max() < 1e-7
     assert np.abs(t[:, half:] - np.cos(ang)).max() < 1e-7
+
+
+def _conv_case(orc, dtype, b, h, w, c_in, c_out, seed):
+    """Random NHWC input, checkpoint-layout weight [c_out][c_in][3][3] and its
+    (kh, kw, ic) permutation padded to ldw = 9 c_in rounded up to 8."""
+    rng = np.random.default_rng(seed)
+    x = _h16(orc, rng.standard_normal((b, h, w, c_in)), dtype)
+    wck = _h16(orc, 0.2 * rng.standard_normal((c_out, c_in, 3, 3)), dtype)
+    ldw = (9 * c_in + 7) // 8 * 8
+    wperm = np.zeros((c_out, ldw), np.uint16)
+    wperm[:, :9 * c_in] = wck.transpose(0, 2, 3, 1).reshape(c_out, 9 * c_in)
+    bias = _h16(orc, 0.1 * rng.standard_normal(c_out), dtype)
+    return x, wck, wperm, bias
+
+
+@pytest.mark.parametrize("dtype", [F16, BF16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("b,h,w,c_in,c_out", [(2, 9, 7, 1, 16), (1, 8, 10, 16, 24),
+                                              (2, 5, 6, 64, 8)])
+def test_conv_matches_torch_conv2d(orc, dtype, b, h, w, c_in, c_out):
+    """The conv definition (stride 2, padding 1, the (kh, kw, ic) weight
+    permutation, both output row orders, bias, erf GELU) against torch's float64
+    conv2d on the same values in NCHW with the checkpoint's weight layout."""
+    import torch
+    x, wck, wperm, bias = _conv_case(orc, dtype, b, h, w, c_in, c_out, b * h + c_in)
+    xt = torch.from_numpy(_f(orc, x, dtype)).permute(0, 3, 1, 2)
+    wt = torch.from_numpy(_f(orc, wck, dtype))
+    bt = torch.from_numpy(_f(orc, bias, dtype))
+    ref = torch.nn.functional.gelu(torch.nn.functional.conv2d(xt, wt, bt, stride=2, padding=1))
+    ho, wo = ref.shape[2], ref.shape[3]
+    assert (ho, wo) == ((h - 1) // 2 + 1, (w - 1) // 2 + 1)
+    for tmajor in (False, True):
+        got = _f(orc, orc.conv3x3s2(dtype, x, wperm, bias, token_major=tmajor), dtype)
+        r = ref.permute(0, 3, 2, 1) if tmajor else ref.permute(0, 2, 3, 1)  # rows (b,wo,ho)/(b,ho,wo)
+        r = r.reshape(-1, c_out).numpy()
+        assert (np.abs(got - r) <= ulp16(r, dtype) + 1e-6).all(), np.abs(got - r).max()
+
+
+def test_conv_matches_the_reference_im2col(orc):
+    """A restatement of the reference's own im2col (src/audio_encoder.rs:
+    204-236: NCHW input, col[ic*9 + kh*3 + kw], ih = 2 ho + kh - 1) times the
+    checkpoint weight [c_out][c_in*9], row order (b, ho, wo)."""
+    b, h, w, c_in, c_out = 2, 7, 6, 3, 8
+    x, wck, wperm, bias = _conv_case(orc, F16, b, h, w, c_in, c_out, 4)
+    xn = _f(orc, x, F16).transpose(0, 3, 1, 2)  # NCHW
+    ho, wo = (h - 1) // 2 + 1, (w - 1) // 2 + 1
+    cols = np.zeros((b * ho * wo, c_in * 9))
+    for i in range(b * ho * wo):
+        ib, rem = divmod(i, ho * wo)
+        oh, ow = divmod(rem, wo)
+        for ic in range(c_in):
+            for kh in range(3):
+                for kw in range(3):
+                    ih, iw = oh * 2 + kh - 1, ow * 2 + kw - 1
+                    if 0 <= ih < h and 0 <= iw < w:
+                        cols[i, ic * 9 + kh * 3 + kw] = xn[ib, ic, ih, iw]
+    pre = cols @ _f(orc, wck, F16).reshape(c_out, c_in * 9).T + _f(orc, bias, F16)
+    got = _f(orc, orc.conv3x3s2(F16, x, wperm, bias, gelu=False), F16)
+    assert (np.abs(got - pre) <= ulp16(pre, F16) + 1e-6).all()
