@@ -175,6 +175,52 @@ def bench_prefill(host, tdec, rows, warmup, steps):
     }
 
 
+AUDIO = dict(layers=18, n_mels=128, cs=100, c_conv=480, d_model=896, nh=14, ffn=3584,
+             out_dim=1024, wlen=104, chunks=300)  # 300 s of 16 kHz audio: 30000 mel frames
+
+
+def bench_audio_tower(host, ctx, dtype, warmup, steps):
+    """The whole audio tower (GpuAudioEncoder::encode) over 300 s of audio:
+    300 mel chunks -> conv stem -> conv_out + position add -> 18 windowed
+    layers -> projector, 3900 tokens, one hipGraph per step; random weights."""
+    A = AUDIO
+    enc = host.AudioEncoder(ctx, dtype, A["layers"], A["chunks"], A["n_mels"], A["cs"],
+                            A["c_conv"], A["d_model"], A["nh"], A["ffn"], A["out_dim"], A["wlen"])
+    g = lambda tid, shape, std: host.synth_normal(9, tid, shape, 0.0, std, dtype)  # noqa: E731
+    cc, dm, ff = A["c_conv"], A["d_model"], A["ffn"]
+    enc.load_conv(0, g(1, (cc, 1, 3, 3), 1 / 3.0), g(2, (cc,), 0.05))
+    enc.load_conv(1, g(3, (cc, cc, 3, 3), (9 * cc) ** -0.5), g(4, (cc,), 0.05))
+    enc.load_conv(2, g(5, (cc, cc, 3, 3), (9 * cc) ** -0.5), g(6, (cc,), 0.05))
+    enc.load_conv_out(g(7, (dm, cc * 16), (cc * 16) ** -0.5), g(8, (dm,), 0.02))
+    ones, zeros = np.ones(dm, np.float32), np.zeros(dm, np.float32)
+    for li in range(A["layers"]):
+        b = 100 + 16 * li
+        enc.load_layer(li, ones, zeros, g(b, (3 * dm, dm), 0.02), g(b + 1, (3 * dm,), 0.02),
+                       g(b + 2, (dm, dm), 0.02), g(b + 3, (dm,), 0.02), ones, zeros,
+                       g(b + 4, (ff, dm), 0.02), g(b + 5, (ff,), 0.02), g(b + 6, (dm, ff), 0.02),
+                       g(b + 7, (dm,), 0.02))
+    enc.load_post(ones, zeros, g(20, (dm, dm), 0.02), g(21, (dm,), 0.02),
+                  g(22, (A["out_dim"], dm), 0.02), g(23, (A["out_dim"],), 0.02))
+    enc.set_mel(host.synth_normal(9, 30, (A["chunks"], A["n_mels"], A["cs"]), 0.0, 1.0, dtype))
+    ev_ms, wall_ms = enc.time(A["chunks"], 0, warmup, steps, use_graph=True)
+    prof = enc.profile(A["chunks"], 0, 2)
+    n = enc.tokens(A["chunks"], 0)
+    enc.close()
+    px = [A["chunks"] * 64 * 50, A["chunks"] * 32 * 25, A["chunks"] * 16 * 13]
+    conv_f = [2 * px[0] * cc * 9, 2 * px[1] * cc * 9 * cc, 2 * px[2] * cc * 9 * cc]
+    lin_f = 2 * n * (A["layers"] * (4 * dm * dm + 2 * dm * ff) + cc * 16 * dm + dm * dm
+                     + dm * A["out_dim"])
+    return {
+        "ms": round(max(ev_ms, wall_ms), 3),
+        "tokens": n,
+        "tflops_total": round((sum(conv_f) + lin_f) / (max(ev_ms, wall_ms) * 1e-3) / 1e12, 1),
+        "phase_ms": {k: round(v, 3) for k, v in prof.items()},
+        "conv2_tflops": round(conv_f[1] / (prof["conv2"] * 1e-3) / 1e12, 1),
+        "conv3_tflops": round(conv_f[2] / (prof["conv3"] * 1e-3) / 1e12, 1),
+        "conv1_out_gbs": round(px[0] * cc * 2 / (prof["conv1"] * 1e-3) / 1e9, 1),
+    }
+
+
 def bench_encoder(pkg, host, ctx, m, warmup, steps):
     dt = pkg.BF16
     d, f, ck = ENC["d_model"], ENC["ffn"], ENC["conv_k"]
@@ -286,6 +332,10 @@ def main():
         detail["config4_ms"] = round(t4, 4)
         detail["config4_tflops"] = round(f4 / (t4 * 1e-3) / 1e12, 1)
         detail["config4_sites_us"] = {k: round(v * 1e3, 2) for k, v in sites4.items()}
+        # the whole audio tower over 300 s (config 5's encoder), f16
+        r = bench_audio_tower(host, ctx, pkg.F16, 1, 3)
+        detail["audio_tower_300s"] = r
+        log(f"[bench] audio tower 300 s: {r}")
     ctx.close()
 
     traffic, traffic_kernel = measured_traffic("gu")

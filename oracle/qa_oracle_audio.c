@@ -127,23 +127,26 @@ void or_conv3x3s2(int dtype, int64_t batch, int64_t h, int64_t w, int64_t c_in, 
                   const uint16_t* x, const uint16_t* weight, int64_t ldw, const uint16_t* bias,
                   int gelu, int tmajor, int64_t m0, int64_t m1, uint16_t* y) {
   const int64_t ho = (h - 1) / 2 + 1, wo = (w - 1) / 2 + 1, plane = ho * wo;
-  (void)batch;
+  const int64_t nx = batch * h * w * c_in, nw = c_out * ldw;
+  float* xf = (float*)malloc((size_t)nx * sizeof(float));
+  float* wf = (float*)malloc((size_t)nw * sizeof(float));
+  or_h16_to_f32_n(x, xf, nx, dtype);
+  or_h16_to_f32_n(weight, wf, nw, dtype);
 #pragma omp parallel for schedule(dynamic, 4)
   for (int64_t m = m0; m < m1; ++m) {
     const int64_t b = m / plane, q = m % plane;
     const int64_t oh = tmajor ? q % ho : q / wo;
     const int64_t ow = tmajor ? q / ho : q % wo;
     for (int64_t oc = 0; oc < c_out; ++oc) {
-      const uint16_t* wr = weight + oc * ldw;
-      double acc = 0.0;
+      const float* wr = wf + oc * ldw;
+      double acc = 0.0;  /* products of two f32 values are exact in f64 */
       for (int kh = 0; kh < 3; ++kh)
         for (int kw = 0; kw < 3; ++kw) {
           const int64_t ih = 2 * oh + kh - 1, iw = 2 * ow + kw - 1;
           if (ih < 0 || ih >= h || iw < 0 || iw >= w) continue;
-          const uint16_t* xp = x + ((b * h + ih) * w + iw) * c_in;
-          const uint16_t* wp = wr + (kh * 3 + kw) * c_in;
-          for (int64_t ic = 0; ic < c_in; ++ic)
-            acc += (double)or_h16_to_f32(xp[ic], dtype) * (double)or_h16_to_f32(wp[ic], dtype);
+          const float* xp = xf + ((b * h + ih) * w + iw) * c_in;
+          const float* wp = wr + (kh * 3 + kw) * c_in;
+          for (int64_t ic = 0; ic < c_in; ++ic) acc += (double)xp[ic] * (double)wp[ic];
         }
       if (bias) acc += (double)or_h16_to_f32(bias[oc], dtype);
       float v = (float)acc;
@@ -151,4 +154,6 @@ void or_conv3x3s2(int dtype, int64_t batch, int64_t h, int64_t w, int64_t c_in, 
       y[(m - m0) * c_out + oc] = or_h16_from_f32(v, dtype);
     }
   }
+  free(xf);
+  free(wf);
 }

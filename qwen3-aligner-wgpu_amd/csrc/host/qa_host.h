@@ -144,6 +144,50 @@ int qah_tdec_time(qah_tdec* t, int rows, int warmup, int steps, int use_graph,
 int qah_tdec_profile_ops(qah_tdec* t, int rows, int steps, double* op_ms);
 void qah_tdec_destroy(qah_tdec* t);
 
+/* ---- the whole audio tower (audio_encoder.cpp) ---- */
+typedef struct qah_aenc qah_aenc;
+/* Qwen3-ASR audio tower (GpuAudioEncoder::encode, src/audio_encoder_gpu.rs:
+ * 1060-1347): n_mels bins in chunks of cs frames, conv stem of c_conv
+ * channels, `layers` transformer layers of d_model = nh x 64 with an ffn-wide
+ * GELU MLP, windows of wlen tokens, projector to out_dim; up to max_chunks
+ * chunks. */
+int qah_aenc_create(qa_ctx* ctx, int dtype, int layers, int n_mels, int cs, int c_conv,
+                    int d_model, int nh, int ffn, int out_dim, int wlen, int max_chunks,
+                    qah_aenc** out);
+/* Conv level 0..2: weight in the checkpoint's [c_out][c_in][3][3] layout, bias [c_out]. */
+int qah_aenc_load_conv(qah_aenc* a, int level, const uint16_t* w, const uint16_t* b);
+/* conv_out: weight [d_model][c_conv * f] in the checkpoint's (c, f) column order. */
+int qah_aenc_load_conv_out(qah_aenc* a, const uint16_t* w, const uint16_t* b);
+/* Layer li: LayerNorm weights / biases f32 [d_model]; qkv_w [3 d_model][d_model]
+ * (fused q|k|v rows) + qkv_b; o; fc1 [ffn][d_model]; fc2 [d_model][ffn]. */
+int qah_aenc_load_layer(qah_aenc* a, int li, const float* ln1_w, const float* ln1_b,
+                        const uint16_t* qkv_w, const uint16_t* qkv_b, const uint16_t* o_w,
+                        const uint16_t* o_b, const float* ln2_w, const float* ln2_b,
+                        const uint16_t* fc1_w, const uint16_t* fc1_b, const uint16_t* fc2_w,
+                        const uint16_t* fc2_b);
+/* ln_post (f32), proj1 [d_model][d_model], proj2 [out_dim][d_model], with biases. */
+int qah_aenc_load_post(qah_aenc* a, const float* ln_w, const float* ln_b, const uint16_t* p1_w,
+                       const uint16_t* p1_b, const uint16_t* p2_w, const uint16_t* p2_b);
+/* Mel chunks [n_chunks][n_mels][cs] (the last zero-padded past its frames). */
+int qah_aenc_set_mel(qah_aenc* a, int n_chunks, const uint16_t* mel);
+/* Tokens of n_chunks chunks whose last has tail_frames frames (0 = full). */
+int64_t qah_aenc_tokens(qah_aenc* a, int n_chunks, int tail_frames);
+/* Enqueue the whole tower (no wait). */
+int qah_aenc_forward(qah_aenc* a, int n_chunks, int tail_frames);
+/* which = 0 out [rows, out_dim], 1 h [rows, d_model] (the residual stream
+ * after the last layer), 2 conv1 / 3 conv2 output rows [rows, c_conv],
+ * 4 conv_out operand [rows, c_conv * f], 5 the last LayerNorm output
+ * [rows, d_model], 6 qkv [rows, 3 d_model], 7 attention [rows, d_model],
+ * 8 fc1 activation [rows, ffn], 9 proj1 activation [rows, d_model]. */
+int qah_aenc_read(qah_aenc* a, int which, int64_t rows, uint16_t* host);
+int qah_aenc_time(qah_aenc* a, int n_chunks, int tail_frames, int warmup, int steps,
+                  int use_graph, double* ms_per_step, double* wall_ms_per_step);
+/* Event-bracketed ms over `steps` forwards: ms[0..2] conv levels, 3 conv_out +
+ * position add, 4..10 the layer ops summed over all layers (LayerNorm, qkv,
+ * attention, out_proj, LayerNorm 2, fc1, fc2), 11 ln_post + projector. */
+int qah_aenc_profile(qah_aenc* a, int n_chunks, int tail_frames, int steps, double* ms);
+void qah_aenc_destroy(qah_aenc* a);
+
 /* Time `iters` back-to-back launches of one descriptor (HIP events around the
  * whole run on the context's stream); ms per launch. */
 int qah_time_linear(qa_ctx* ctx, const qa_linear_desc* desc, int warmup, int iters,

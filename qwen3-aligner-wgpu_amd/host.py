@@ -57,6 +57,20 @@ def declare(L: ctypes.CDLL) -> None:
     L.qah_tdec_profile_ops.argtypes = [_vp, _i, _i, _dp]
     L.qah_tdec_destroy.argtypes = [_vp]
     L.qah_tdec_destroy.restype = None
+    L.qah_aenc_create.argtypes = [_vp] + [_i] * 11 + [ctypes.POINTER(_vp)]
+    L.qah_aenc_load_conv.argtypes = [_vp, _i, _vp, _vp]
+    L.qah_aenc_load_conv_out.argtypes = [_vp, _vp, _vp]
+    L.qah_aenc_load_layer.argtypes = [_vp, _i] + [_vp] * 12
+    L.qah_aenc_load_post.argtypes = [_vp] + [_vp] * 6
+    L.qah_aenc_set_mel.argtypes = [_vp, _i, _vp]
+    L.qah_aenc_tokens.argtypes = [_vp, _i, _i]
+    L.qah_aenc_tokens.restype = ctypes.c_int64
+    L.qah_aenc_forward.argtypes = [_vp, _i, _i]
+    L.qah_aenc_read.argtypes = [_vp, _i, ctypes.c_int64, _vp]
+    L.qah_aenc_time.argtypes = [_vp, _i, _i, _i, _i, _i, _dp, _dp]
+    L.qah_aenc_profile.argtypes = [_vp, _i, _i, _i, _dp]
+    L.qah_aenc_destroy.argtypes = [_vp]
+    L.qah_aenc_destroy.restype = None
     del _fp
     L.qah_time_linear.argtypes = [_vp, _vp, _i, _i, _dp]
     L.qah_copy_calibration.argtypes = [_vp, _sz, _i]
@@ -68,7 +82,10 @@ def declare(L: ctypes.CDLL) -> None:
                  "qah_time_linear", "qah_copy_calibration", "qah_tdec_create",
                  "qah_tdec_load_layer", "qah_tdec_set_rope", "qah_tdec_set_attention_flags",
                  "qah_tdec_set_hidden", "qah_tdec_prefill", "qah_tdec_read", "qah_tdec_time",
-                 "qah_tdec_profile_ops"):
+                 "qah_tdec_profile_ops", "qah_aenc_create", "qah_aenc_load_conv",
+                 "qah_aenc_load_conv_out", "qah_aenc_load_layer", "qah_aenc_load_post",
+                 "qah_aenc_set_mel", "qah_aenc_forward", "qah_aenc_read", "qah_aenc_time",
+                 "qah_aenc_profile"):
         getattr(L, name).restype = _i
 
 
@@ -280,6 +297,93 @@ class TextDecoder:
         out = (ctypes.c_double * 8)()
         check(host_lib().qah_tdec_profile_ops(self.handle, rows, steps, out))
         return dict(zip(self.OPS, list(out)))
+
+
+class AudioEncoder:
+    """qah_aenc: the whole audio tower (conv stem, conv_out + position add,
+    windowed-attention layers, projector), GpuAudioEncoder::encode."""
+
+    READS = {"out": 0, "h": 1, "conv1": 2, "conv2": 3, "conv3": 4, "normed": 5, "qkv": 6,
+             "attn": 7, "act": 8, "pact": 9}
+    PROFILE = ("conv1", "conv2", "conv3", "conv_out_pe", "ln1", "qkv", "attention", "o", "ln2",
+               "fc1", "fc2", "post")
+
+    def __init__(self, ctx, dtype: int, layers: int, max_chunks: int, n_mels: int = 128,
+                 cs: int = 100, c_conv: int = 480, d_model: int = 896, nh: int = 14,
+                 ffn: int = 3584, out_dim: int = 1024, wlen: int = 104):
+        self.ctx, self.dtype, self.layers, self.max_chunks = ctx, dtype, layers, max_chunks
+        self.n_mels, self.cs, self.c_conv, self.d_model = n_mels, cs, c_conv, d_model
+        self.nh, self.ffn, self.out_dim, self.wlen = nh, ffn, out_dim, wlen
+        f = lambda v: (v - 1) // 2 + 1  # noqa: E731
+        self.h3, self.w3 = f(f(f(n_mels))), f(f(f(cs)))
+        h = _vp()
+        check(host_lib().qah_aenc_create(ctx.handle, dtype, layers, n_mels, cs, c_conv, d_model,
+                                         nh, ffn, out_dim, wlen, max_chunks, ctypes.byref(h)))
+        self.handle = h.value
+
+    def close(self):
+        if self.handle:
+            host_lib().qah_aenc_destroy(self.handle)
+            self.handle = None
+
+    @staticmethod
+    def _u16(*arrs):
+        return [np.ascontiguousarray(a, np.uint16) for a in arrs]
+
+    @staticmethod
+    def _f32(*arrs):
+        return [np.ascontiguousarray(a, np.float32) for a in arrs]
+
+    def load_conv(self, level, w, b):
+        w, b = self._u16(w, b)
+        check(host_lib().qah_aenc_load_conv(self.handle, level, _p(w), _p(b)))
+
+    def load_conv_out(self, w, b):
+        w, b = self._u16(w, b)
+        check(host_lib().qah_aenc_load_conv_out(self.handle, _p(w), _p(b)))
+
+    def load_layer(self, li, ln1_w, ln1_b, qkv_w, qkv_b, o_w, o_b, ln2_w, ln2_b, fc1_w, fc1_b,
+                   fc2_w, fc2_b):
+        l1w, l1b, l2w, l2b = self._f32(ln1_w, ln1_b, ln2_w, ln2_b)
+        ws = self._u16(qkv_w, qkv_b, o_w, o_b, fc1_w, fc1_b, fc2_w, fc2_b)
+        check(host_lib().qah_aenc_load_layer(self.handle, li, _p(l1w), _p(l1b), _p(ws[0]),
+                                             _p(ws[1]), _p(ws[2]), _p(ws[3]), _p(l2w), _p(l2b),
+                                             _p(ws[4]), _p(ws[5]), _p(ws[6]), _p(ws[7])))
+
+    def load_post(self, ln_w, ln_b, p1_w, p1_b, p2_w, p2_b):
+        lw, lb = self._f32(ln_w, ln_b)
+        ws = self._u16(p1_w, p1_b, p2_w, p2_b)
+        check(host_lib().qah_aenc_load_post(self.handle, _p(lw), _p(lb), *[_p(a) for a in ws]))
+
+    def set_mel(self, mel):
+        mel = np.ascontiguousarray(mel, np.uint16)
+        check(host_lib().qah_aenc_set_mel(self.handle, mel.shape[0], _p(mel)))
+
+    def tokens(self, n_chunks, tail_frames=0) -> int:
+        return int(host_lib().qah_aenc_tokens(self.handle, n_chunks, tail_frames))
+
+    def forward(self, n_chunks, tail_frames=0):
+        check(host_lib().qah_aenc_forward(self.handle, n_chunks, tail_frames))
+
+    def read(self, which: str, rows: int) -> np.ndarray:
+        cols = {"out": self.out_dim, "h": self.d_model, "conv1": self.c_conv,
+                "conv2": self.c_conv, "conv3": self.c_conv * self.h3, "normed": self.d_model,
+                "qkv": 3 * self.d_model, "attn": self.d_model, "act": self.ffn,
+                "pact": self.d_model}[which]
+        out = np.empty((rows, cols), np.uint16)
+        check(host_lib().qah_aenc_read(self.handle, self.READS[which], rows, out.ctypes.data))
+        return out
+
+    def time(self, n_chunks, tail_frames, warmup, steps, use_graph=True) -> tuple[float, float]:
+        ms, wall = ctypes.c_double(), ctypes.c_double()
+        check(host_lib().qah_aenc_time(self.handle, n_chunks, tail_frames, warmup, steps,
+                                       int(use_graph), ctypes.byref(ms), ctypes.byref(wall)))
+        return ms.value, wall.value
+
+    def profile(self, n_chunks, tail_frames, steps) -> dict:
+        out = (ctypes.c_double * 12)()
+        check(host_lib().qah_aenc_profile(self.handle, n_chunks, tail_frames, steps, out))
+        return dict(zip(self.PROFILE, list(out)))
 
 
 def time_linear(ctx, desc, warmup: int, iters: int) -> float:
