@@ -340,6 +340,34 @@ typedef struct qa_position_add_desc {
 } qa_position_add_desc;
 int qa_add_position_table(qa_ctx* ctx, const qa_position_add_desc* desc);
 
+/* ---- the aligner's host-side formats, on the device ---- */
+
+/* The slaney mel filterbank [n_mels][n_fft / 2 + 1] (f32, slaney scale and
+ * area normalisation, 0 Hz .. sample_rate / 2), create_mel_filterbank
+ * (src/mel.rs:100-154).  Host function, no device needed; returns QA_EINVAL
+ * on a null output or non-positive sizes. */
+int qa_mel_filterbank(int n_mels, int n_fft, int sample_rate, float* out);
+
+/* Log-mel of 16 kHz samples straight into the audio tower's input chunks:
+ * centered STFT (n_fft 400, hop 160, periodic Hann, reflect padding), power,
+ * the filterbank, log10(max(., 1e-10)), clamp to (clip max - 8), (x + 4) / 4
+ * (MelExtractor::extract, src/mel.rs:203-243), frames = n_samples / 160.
+ * out [ceil(frames / cs)][n_mels][cs] in the 16-bit format, frames past the
+ * last zero (the chunking of encode, src/audio_encoder_gpu.rs:1079-1091).
+ * samples and filterbank are device f32 buffers; needs n_samples >= 160
+ * (at least one frame) and cs even.  Uses the context's workspace
+ * (n_mels * frames floats), which grows only outside graph capture. */
+typedef struct qa_mel_desc {
+  uint32_t dtype;
+  uint32_t flags; /* reserved, must be 0 */
+  int64_t n_samples;
+  const float* samples;
+  const float* filterbank;
+  int32_t n_mels, cs;
+  void* out;
+} qa_mel_desc;
+int qa_log_mel(qa_ctx* ctx, const qa_mel_desc* desc);
+
 /* Message of the last failure on this thread ("" if none). */
 const char* qa_last_error(void);
 /* Library version string, e.g. "qa 0.1.0 (abi 1, gfx950)". */

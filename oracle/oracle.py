@@ -100,6 +100,12 @@ def lib() -> ctypes.CDLL:
         L.or_sinusoid_table.restype = None
         L.or_conv3x3s2.argtypes = [ci, i64, i64, i64, i64, i64, p, p, i64, p, ci, ci, i64, i64, p]
         L.or_conv3x3s2.restype = None
+        L.or_mel_filterbank.argtypes = [ci, ci, ci, p]
+        L.or_mel_filterbank.restype = None
+        L.or_stft_power.argtypes = [p, i64, ci, ci, p]
+        L.or_stft_power.restype = None
+        L.or_log_mel.argtypes = [p, i64, ci, p, p]
+        L.or_log_mel.restype = None
         L.or_vperm.restype = i64
         L.or_num_threads.restype = ctypes.c_int
         _lib = L
@@ -311,3 +317,27 @@ def conv3x3s2(dtype: int, x: np.ndarray, weight: np.ndarray, bias: np.ndarray | 
                        _ptr(bb) if bb is not None else None, int(gelu), int(token_major), m0, m1,
                        _ptr(y))
     return y
+
+
+def mel_filterbank(n_mels: int = 128, n_fft: int = 400, sr: int = 16000) -> np.ndarray:
+    """or_mel_filterbank -> [n_mels, n_fft // 2 + 1] f32."""
+    out = np.empty((n_mels, n_fft // 2 + 1), np.float32)
+    lib().or_mel_filterbank(n_mels, n_fft, sr, _ptr(out))
+    return out
+
+
+def stft_power(x: np.ndarray, n_fft: int = 400, hop: int = 160) -> np.ndarray:
+    """or_stft_power -> [frames, n_fft // 2 + 1] f64."""
+    x = _c(x, np.float32)
+    out = np.empty((x.size // hop, n_fft // 2 + 1), np.float64)
+    lib().or_stft_power(_ptr(x), x.size, n_fft, hop, _ptr(out))
+    return out
+
+
+def log_mel(x: np.ndarray, filt: np.ndarray | None = None, n_mels: int = 128) -> np.ndarray:
+    """or_log_mel -> [n_mels, frames] f32 (before the 16-bit rounding)."""
+    x = _c(x, np.float32)
+    filt = mel_filterbank(n_mels) if filt is None else _c(filt, np.float32)
+    out = np.empty((n_mels, x.size // 160), np.float32)
+    lib().or_log_mel(_ptr(x), x.size, n_mels, _ptr(filt), _ptr(out))
+    return out

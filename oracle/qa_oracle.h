@@ -132,6 +132,14 @@ void or_sinusoid_table(int64_t positions, int64_t dm, float* table);
 void or_conv3x3s2(int dtype, int64_t batch, int64_t h, int64_t w, int64_t c_in, int64_t c_out,
                   const uint16_t* x, const uint16_t* weight, int64_t ldw, const uint16_t* bias,
                   int gelu, int tmajor, int64_t m0, int64_t m1, uint16_t* y);
+/* The log-mel front end (src/mel.rs).  Pins (tests/test_oracle_mel.py):
+ * numpy's rfft of the same reflect-padded Hann-windowed frames, the slaney
+ * scale's fixed points (1 kHz = mel 15, mel <-> Hz round trip), each filter a
+ * triangle of unit area, a pure tone peaking in the bin that holds it, and
+ * the uniform log10(c^2) / 4 shift of a signal scaled by c. */
+void or_mel_filterbank(int n_mels, int n_fft, int sr, float* out);
+void or_stft_power(const float* x, int64_t n, int n_fft, int hop, double* power);
+void or_log_mel(const float* x, int64_t n, int n_mels, const float* filt, float* out);
 
 #ifdef __cplusplus
 }

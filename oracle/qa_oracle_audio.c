@@ -157,3 +157,106 @@ void or_conv3x3s2(int dtype, int64_t batch, int64_t h, int64_t w, int64_t c_in, 
   free(xf);
   free(wf);
 }
+
+/* create_mel_filterbank (src/mel.rs:100-154), restated: slaney mel scale
+ * (linear below 1 kHz at 200/3 Hz per mel, logarithmic above with step
+ * ln(6.4) / 27), n_mels + 2 points evenly spaced in mel over 0 .. sr / 2,
+ * triangles over bin frequencies j sr / n_fft, each scaled by
+ * 2 / (f[i+2] - f[i]); f64 math, f32 storage and f32 scaling. */
+static double or_hz_to_mel(double f) {
+  const double f_sp = 200.0 / 3.0, min_log_hz = 1000.0, logstep = log(6.4) / 27.0;
+  return f < min_log_hz ? f / f_sp : min_log_hz / f_sp + log(f / min_log_hz) / logstep;
+}
+static double or_mel_to_hz(double m) {
+  const double f_sp = 200.0 / 3.0, min_log_hz = 1000.0, logstep = log(6.4) / 27.0;
+  const double min_log_mel = min_log_hz / f_sp;
+  return m < min_log_mel ? f_sp * m : min_log_hz * exp(logstep * (m - min_log_mel));
+}
+void or_mel_filterbank(int n_mels, int n_fft, int sr, float* out) {
+  const int nf = n_fft / 2 + 1;
+  double* ff = (double*)malloc(sizeof(double) * (size_t)(n_mels + 2));
+  const double lo = or_hz_to_mel(0.0), hi = or_hz_to_mel(sr / 2.0);
+  for (int i = 0; i < n_mels + 2; ++i) ff[i] = or_mel_to_hz(lo + (hi - lo) * i / (double)(n_mels + 1));
+  for (int i = 0; i < n_mels; ++i)
+    for (int j = 0; j < nf; ++j) {
+      const double f = (double)j * sr / n_fft;
+      const double down = (f - ff[i]) / (ff[i + 1] - ff[i]);
+      const double up = (ff[i + 2] - f) / (ff[i + 2] - ff[i + 1]);
+      double v = down < up ? down : up;
+      if (v < 0.0) v = 0.0;
+      out[i * nf + j] = (float)v * (float)(2.0 / (ff[i + 2] - ff[i]));
+    }
+  free(ff);
+}
+
+/* |X_k|^2 of the centered STFT (src/mel.rs:47-98,203-214): reflect padding of
+ * n_fft / 2 without repeating the edge, periodic Hann 0.5 (1 - cos(2 pi j /
+ * n_fft)), frames every hop samples, the last frame dropped; a direct DFT in
+ * f64.  power [frames][n_fft / 2 + 1], frames = n / hop. */
+void or_stft_power(const float* x, int64_t n, int n_fft, int hop, double* power) {
+  const int nf = n_fft / 2 + 1;
+  const int64_t frames = n / hop, pad = n_fft / 2;
+  double* cs = (double*)malloc(sizeof(double) * (size_t)n_fft);
+  double* sn = (double*)malloc(sizeof(double) * (size_t)n_fft);
+  for (int j = 0; j < n_fft; ++j) {
+    cs[j] = cos(2.0 * 3.14159265358979323846 * j / n_fft);
+    sn[j] = sin(2.0 * 3.14159265358979323846 * j / n_fft);
+  }
+#pragma omp parallel for schedule(static)
+  for (int64_t f = 0; f < frames; ++f) {
+    double fr[4096];
+    for (int j = 0; j < n_fft; ++j) {
+      int64_t i = f * hop + j - pad;
+      const int64_t period = 2 * (n - 1);
+      if (n > 1) {
+        i %= period;
+        if (i < 0) i += period;
+        if (i > n - 1) i = period - i;
+      } else {
+        i = 0;
+      }
+      fr[j] = (double)x[i] * 0.5 * (1.0 - cs[j]);
+    }
+    for (int k = 0; k < nf; ++k) {
+      double re = 0.0, im = 0.0;
+      int idx = 0;
+      for (int j = 0; j < n_fft; ++j) {
+        re += fr[j] * cs[idx];
+        im -= fr[j] * sn[idx];
+        idx += k;
+        if (idx >= n_fft) idx -= n_fft;
+      }
+      power[f * nf + k] = re * re + im * im;
+    }
+  }
+  free(cs);
+  free(sn);
+}
+
+/* The log-mel of MelExtractor::extract (src/mel.rs:203-243) with n_fft 400,
+ * hop 160: mel = filterbank . power (f64), log10(max(mel, 1e-10)), clamp at
+ * (max over the clip) - 8, (x + 4) / 4.  out f32 [n_mels][frames]. */
+void or_log_mel(const float* x, int64_t n, int n_mels, const float* filt, float* out) {
+  const int n_fft = 400, hop = 160, nf = n_fft / 2 + 1;
+  const int64_t frames = n / hop;
+  double* power = (double*)malloc(sizeof(double) * (size_t)(frames * nf));
+  or_stft_power(x, n, n_fft, hop, power);
+  double* lm = (double*)malloc(sizeof(double) * (size_t)(frames * n_mels));
+  double mx = -INFINITY;
+#pragma omp parallel for schedule(static) reduction(max : mx)
+  for (int64_t f = 0; f < frames; ++f)
+    for (int m = 0; m < n_mels; ++m) {
+      double acc = 0.0;
+      for (int k = 0; k < nf; ++k) acc += (double)filt[m * nf + k] * power[f * nf + k];
+      const double v = log10(acc > 1e-10 ? acc : 1e-10);
+      lm[f * n_mels + m] = v;
+      if (v > mx) mx = v;
+    }
+  for (int m = 0; m < n_mels; ++m)
+    for (int64_t f = 0; f < frames; ++f) {
+      const double v = lm[f * n_mels + m];
+      out[m * frames + f] = (float)(((v > mx - 8.0 ? v : mx - 8.0) + 4.0) / 4.0);
+    }
+  free(power);
+  free(lm);
+}

@@ -219,12 +219,28 @@ class ConvDesc(ctypes.Structure):
     ]
 
 
+class MelDesc(ctypes.Structure):
+    """qa_mel_desc (include/qa.h)."""
+
+    _fields_ = [
+        ("dtype", ctypes.c_uint32),
+        ("flags", ctypes.c_uint32),
+        ("n_samples", ctypes.c_int64),
+        ("samples", ctypes.c_void_p),
+        ("filterbank", ctypes.c_void_p),
+        ("n_mels", ctypes.c_int32),
+        ("cs", ctypes.c_int32),
+        ("out", ctypes.c_void_p),
+    ]
+
+
 # Every symbol include/qa.h declares (checked by tests/test_abi.py).
 EXPORTS = (
     "qa_ctx_create", "qa_ctx_destroy", "qa_ctx_stream", "qa_alloc", "qa_free",
     "qa_upload", "qa_download", "qa_sync", "qa_linear", "qa_linear_validate",
     "qa_mlp_fused", "qa_rms_norm", "qa_qk_norm_rope", "qa_attention_prefill",
     "qa_layer_norm", "qa_window_attention", "qa_add_position_table", "qa_conv2d_3x3s2",
+    "qa_mel_filterbank", "qa_log_mel",
     "qa_last_error", "qa_version",
 )
 
@@ -259,6 +275,8 @@ def lib() -> ctypes.CDLL:
         L.qa_window_attention.argtypes = [vp, ctypes.POINTER(WindowAttentionDesc)]
         L.qa_add_position_table.argtypes = [vp, ctypes.POINTER(PositionAddDesc)]
         L.qa_conv2d_3x3s2.argtypes = [vp, ctypes.POINTER(ConvDesc)]
+        L.qa_mel_filterbank.argtypes = [i, i, i, vp]
+        L.qa_log_mel.argtypes = [vp, ctypes.POINTER(MelDesc)]
         L.qa_last_error.restype = ctypes.c_char_p
         L.qa_version.restype = ctypes.c_char_p
         for name in EXPORTS:
@@ -381,6 +399,16 @@ class Context:
 
     def conv2d_3x3s2(self, desc: ConvDesc) -> None:
         check(lib().qa_conv2d_3x3s2(self.handle, ctypes.byref(desc)))
+
+    def log_mel(self, desc: MelDesc) -> None:
+        check(lib().qa_log_mel(self.handle, ctypes.byref(desc)))
+
+
+def mel_filterbank(n_mels: int = 128, n_fft: int = 400, sample_rate: int = 16000) -> np.ndarray:
+    """qa_mel_filterbank (host): the slaney filterbank [n_mels, n_fft // 2 + 1] f32."""
+    out = np.empty((n_mels, n_fft // 2 + 1), np.float32)
+    check(lib().qa_mel_filterbank(n_mels, n_fft, sample_rate, out.ctypes.data))
+    return out
 
 
 def linear_desc(dtype: int, m: int, n: int, k: int, a, w, c, *, flags: int = 0, bias=None,

@@ -8,11 +8,13 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <string>
+#include <vector>
 
 #include "qa.h"
 #include "qa_internal.h"
@@ -270,8 +272,8 @@ int ensure_workspace(qa_ctx* ctx, size_t floats) {
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
   if (hipStreamIsCapturing(ctx->stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
     return fail(QA_EINVAL,
-                "qa_linear: the split-K workspace must grow (%zu floats) but the stream is "
-                "being captured; run the same call once before capture",
+                "the context workspace must grow (%zu floats) but the stream is being "
+                "captured; run the same call once before capture",
                 floats);
   hipError_t e = hipStreamSynchronize(ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
@@ -279,7 +281,7 @@ int ensure_workspace(qa_ctx* ctx, size_t floats) {
   ctx->ws = nullptr;
   ctx->ws_floats = 0;
   e = hipMalloc(&ctx->ws, floats * sizeof(float));
-  if (e != hipSuccess) return hip_fail(e, "hipMalloc(split-K workspace)");
+  if (e != hipSuccess) return hip_fail(e, "hipMalloc(context workspace)");
   ctx->ws_floats = floats;
   return ok();
 }
@@ -668,6 +670,68 @@ int qa_conv2d_3x3s2(qa_ctx* ctx, const qa_conv_desc* d) {
   p.cv_tmajor = tmajor;
   const hipError_t e = qa::launch_gemm((int)d->dtype, plan, p, 1, ctx->stream);
   return e == hipSuccess ? ok() : hip_fail(e, "qa_conv2d_3x3s2 launch");
+}
+
+int qa_mel_filterbank(int n_mels, int n_fft, int sample_rate, float* out) {
+  if (!out || n_mels <= 0 || n_fft <= 0 || sample_rate <= 0)
+    return fail(QA_EINVAL, "qa_mel_filterbank: bad argument");
+  // create_mel_filterbank (src/mel.rs:100-154): slaney mel scale (linear below
+  // 1 kHz at 200/3 Hz per mel, logarithmic above with step ln(6.4) / 27),
+  // n_mels + 2 points evenly spaced in mel from 0 to sr / 2, triangles over
+  // the FFT bin frequencies, each scaled by 2 / (width in Hz).  f64, stored f32.
+  const int n_freqs = n_fft / 2 + 1;
+  const double sr = sample_rate, f_sp = 200.0 / 3.0, min_log_hz = 1000.0;
+  const double min_log_mel = min_log_hz / f_sp, logstep = std::log(6.4) / 27.0;
+  auto hz_to_mel = [&](double f) {
+    return f < min_log_hz ? f / f_sp : min_log_mel + std::log(f / min_log_hz) / logstep;
+  };
+  auto mel_to_hz = [&](double m) {
+    return m < min_log_mel ? f_sp * m : min_log_hz * std::exp(logstep * (m - min_log_mel));
+  };
+  const double mel_lo = hz_to_mel(0.0), mel_hi = hz_to_mel(sr / 2.0);
+  std::vector<double> ff((size_t)n_mels + 2);
+  for (int i = 0; i < n_mels + 2; ++i)
+    ff[(size_t)i] = mel_to_hz(mel_lo + (mel_hi - mel_lo) * i / (double)(n_mels + 1));
+  for (int i = 0; i < n_mels; ++i) {
+    const double enorm = 2.0 / (ff[(size_t)i + 2] - ff[(size_t)i]);
+    for (int j = 0; j < n_freqs; ++j) {
+      const double f = j * sr / n_fft;
+      const double down = (f - ff[(size_t)i]) / (ff[(size_t)i + 1] - ff[(size_t)i]);
+      const double up = (ff[(size_t)i + 2] - f) / (ff[(size_t)i + 2] - ff[(size_t)i + 1]);
+      out[(size_t)i * n_freqs + j] = (float)std::max(0.0, std::min(down, up)) * (float)enorm;
+    }
+  }
+  return ok();
+}
+
+int qa_log_mel(qa_ctx* ctx, const qa_mel_desc* d) {
+  if (!ctx || !d) return fail(QA_EINVAL, "qa_log_mel: null argument");
+  if (d->dtype != QA_F16 && d->dtype != QA_BF16)
+    return fail(QA_EINVAL, "qa_log_mel: dtype %u is neither QA_F16 nor QA_BF16", d->dtype);
+  if (d->flags) return fail(QA_EINVAL, "qa_log_mel: flags must be 0");
+  if (d->n_samples < 160 || d->n_samples > kI32 || d->n_mels <= 0 || d->n_mels > 1024 ||
+      d->cs <= 0 || d->cs % 2)
+    return fail(QA_EINVAL, "qa_log_mel: need n_samples >= 160, 0 < n_mels <= 1024 and cs even");
+  if (!d->samples || !d->filterbank || !d->out) return fail(QA_EINVAL, "qa_log_mel: null pointer");
+  if (!aligned(d->samples, 4) || !aligned(d->filterbank, 4) || !aligned(d->out, 4))
+    return fail(QA_EINVAL, "qa_log_mel: misaligned pointer");
+  if (int rc = set_device(ctx)) return rc;
+  qa::MelParams p{};
+  p.frames = d->n_samples / 160;
+  p.n = d->n_samples;
+  p.n_mels = d->n_mels;
+  p.cs = d->cs;
+  p.n_chunks = (int)((p.frames + d->cs - 1) / d->cs);
+  p.nblocks = (int)((p.frames + 15) / 16);
+  const size_t floats = (size_t)p.n_mels * (size_t)p.frames + (size_t)p.nblocks;
+  if (int rc = ensure_workspace(ctx, floats)) return rc;
+  p.x = d->samples;
+  p.filt = d->filterbank;
+  p.logmel = ctx->ws;
+  p.bmax = ctx->ws + (size_t)p.n_mels * (size_t)p.frames;
+  p.out = (uint16_t*)d->out;
+  const hipError_t e = qa::launch_log_mel((int)d->dtype, p, ctx->stream);
+  return e == hipSuccess ? ok() : hip_fail(e, "qa_log_mel launch");
 }
 
 int qa_layer_norm(qa_ctx* ctx, const qa_layer_norm_desc* d) {

@@ -163,6 +163,18 @@ struct Conv1Params {
 };
 hipError_t launch_conv1(int dtype, const Conv1Params& p, hipStream_t stream);
 
+// Log-mel front end (qa_mel.hip).
+struct MelParams {
+  const float* x;      // samples [n]
+  const float* filt;   // [n_mels][201]
+  float* logmel;       // workspace [n_mels][frames]
+  float* bmax;         // workspace [nblocks]
+  uint16_t* out;       // [n_chunks][n_mels][cs]
+  int64_t n, frames;
+  int n_mels, cs, n_chunks, nblocks;
+};
+hipError_t launch_log_mel(int dtype, const MelParams& p, hipStream_t stream);
+
 // p16: probabilities rounded once to the 16-bit format (else two 16-bit terms).
 hipError_t launch_attention(int dtype, const AttnParams& p, bool p16, hipStream_t stream);
 

@@ -1,0 +1,156 @@
+// qa_mel.hip -- the aligner's log-mel front end on the GPU: 16 kHz samples ->
+// centered STFT (n_fft 400, hop 160, periodic Hann, reflect padding) ->
+// power -> 128 slaney mel bins -> log10 clamped to max - 8 -> (x + 4) / 4,
+// written as the audio tower's 16-bit mel chunks (MelExtractor::extract,
+// src/mel.rs:203-243; chunking, src/audio_encoder_gpu.rs:1079-1091).  The
+// reference runs this on the CPU with an f32 FFT; here a block transforms 16
+// frames at once as a direct DFT from LDS (400 x 201 multiply-adds per
+// frame, ~5 GFLOP for 300 s, far below the towers' cost), accumulated in f64:
+// an f32 direct DFT would lose relative accuracy on bins 6+ decades below the
+// frame's peak, which the log-mel keeps (its floor is the clip max - 8), so
+// the transform is made effectively exact and the mel, log and clamp run in
+// f32 like the reference's.
+#include <algorithm>
+
+#include "qa_internal.h"
+
+namespace qa {
+namespace {
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+constexpr int NFFT = 400, HOP = 160, NBIN = NFFT / 2 + 1, FB = 16;
+
+// Reflection index without repeating the edge (src/mel.rs:27-45).
+__device__ __forceinline__ int64_t reflect(int64_t i, int64_t n) {
+  if (n <= 1) return 0;
+  const int64_t period = 2 * (n - 1);
+  int64_t x = i % period;
+  if (x < 0) x += period;
+  return x > n - 1 ? period - x : x;
+}
+
+// Frames f0..f0+15: windowed samples in LDS, power spectra, mel bins, log10.
+__global__ void __launch_bounds__(256) mel_log_kernel(const MelParams p) {
+  __shared__ float xw[FB][NFFT];
+  __shared__ float pw[FB][NBIN + 3];
+  __shared__ double tc[NFFT], ts[NFFT];
+  __shared__ float red[256];
+  const int tid = threadIdx.x;
+  const int64_t f0 = (int64_t)blockIdx.x * FB;
+  for (int j = tid; j < NFFT; j += 256) {
+    // twiddles e^{-2 pi i j / 400} and the periodic Hann window 0.5 (1 - cos(2 pi j / 400))
+    double s, c;
+    sincospi((double)(2 * j) / (double)NFFT, &s, &c);
+    tc[j] = c;
+    ts[j] = s;
+  }
+  __syncthreads();
+  for (int i = tid; i < FB * NFFT; i += 256) {
+    const int f = i / NFFT, j = i - f * NFFT;
+    float v = 0.f;
+    if (f0 + f < p.frames) {
+      // centered frame: padded sample (f0 + f) * hop + j = original index - n_fft / 2
+      const int64_t src = reflect((f0 + f) * HOP + j - NFFT / 2, p.n);
+      v = p.x[src] * (float)(0.5 * (1.0 - tc[j]));
+    }
+    xw[f][j] = v;
+  }
+  __syncthreads();
+  // one thread per bin k: the 16 frames' DFT at k, twiddle index j k mod 400
+  if (tid < NBIN) {
+    const int k = tid;
+    double re[FB], im[FB];
+#pragma unroll
+    for (int f = 0; f < FB; ++f) re[f] = im[f] = 0.0;
+    int idx = 0;
+    for (int j = 0; j < NFFT; ++j) {
+      const double c = tc[idx], s = ts[idx];
+#pragma unroll
+      for (int f = 0; f < FB; ++f) {
+        re[f] += (double)xw[f][j] * c;
+        im[f] -= (double)xw[f][j] * s;
+      }
+      idx += k;
+      if (idx >= NFFT) idx -= NFFT;
+    }
+#pragma unroll
+    for (int f = 0; f < FB; ++f) pw[f][k] = (float)(re[f] * re[f] + im[f] * im[f]);
+  }
+  __syncthreads();
+  // mel m of frame f: sum_k filt[m][k] pw[f][k]; log10(max(., 1e-10))
+  float mx = -INFINITY;
+  for (int i = tid; i < p.n_mels * FB; i += 256) {
+    const int m = i % p.n_mels, f = i / p.n_mels;
+    if (f0 + f >= p.frames) continue;
+    const float* fr = p.filt + (int64_t)m * NBIN;
+    float acc = 0.f;
+    for (int k = 0; k < NBIN; ++k) acc += fr[k] * pw[f][k];
+    const float v = logf(fmaxf(acc, 1e-10f)) * (1.0f / 2.302585092994046f);
+    p.logmel[(int64_t)m * p.frames + f0 + f] = v;
+    mx = fmaxf(mx, v);
+  }
+  red[tid] = mx;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if (tid < o) red[tid] = fmaxf(red[tid], red[tid + o]);
+    __syncthreads();
+  }
+  if (tid == 0) p.bmax[blockIdx.x] = red[0];
+}
+
+template <int DT>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {  // RNE
+  if constexpr (DT == QA_F16)
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, f16x2));
+  else
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, bf16x2));
+}
+
+// out[c][m][j] = r16((max(logmel[m][c cs + j], max - 8) + 4) / 4) for valid
+// frames, 0 past them (the zero-padded last chunk); two frames per thread.
+template <int DT>
+__global__ void __launch_bounds__(256) mel_finalize_kernel(const MelParams p) {
+  __shared__ float red[256];
+  float mx = -INFINITY;
+  for (int i = threadIdx.x; i < p.nblocks; i += 256) mx = fmaxf(mx, p.bmax[i]);
+  red[threadIdx.x] = mx;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if ((int)threadIdx.x < o) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + o]);
+    __syncthreads();
+  }
+  const float lo = red[0] - 8.0f;
+  const int64_t pairs = (int64_t)p.n_chunks * p.n_mels * p.cs / 2;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < pairs;
+       i += (int64_t)gridDim.x * 256) {
+    const int64_t e = 2 * i;
+    const int64_t c = e / ((int64_t)p.n_mels * p.cs), r = e - c * p.n_mels * p.cs;
+    const int m = (int)(r / p.cs), j = (int)(r - (int64_t)m * p.cs);
+    float v[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int64_t t = c * p.cs + j + u;
+      v[u] = t < p.frames ? (fmaxf(p.logmel[(int64_t)m * p.frames + t], lo) + 4.0f) / 4.0f : 0.f;
+    }
+    *reinterpret_cast<uint32_t*>(p.out + e) = pack2<DT>(v[0], v[1]);
+  }
+}
+
+}  // namespace
+
+hipError_t launch_log_mel(int dtype, const MelParams& p, hipStream_t s) {
+  hipLaunchKernelGGL(mel_log_kernel, dim3((unsigned)p.nblocks), dim3(256), 0, s, p);
+  const int64_t pairs = (int64_t)p.n_chunks * p.n_mels * p.cs / 2;
+  const unsigned blocks = (unsigned)std::min<int64_t>((pairs + 255) / 256, 4096);
+  if (dtype == QA_BF16)
+    hipLaunchKernelGGL(mel_finalize_kernel<QA_BF16>, dim3(blocks), dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL(mel_finalize_kernel<QA_F16>, dim3(blocks), dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
+}  // namespace qa

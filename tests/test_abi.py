@@ -109,7 +109,8 @@ def test_calls_without_context_fail_cleanly(pkg):
                      (lib.qa_layer_norm, pkg.LayerNormDesc()),
                      (lib.qa_window_attention, pkg.WindowAttentionDesc()),
                      (lib.qa_add_position_table, pkg.PositionAddDesc()),
-                     (lib.qa_conv2d_3x3s2, pkg.ConvDesc())):
+                     (lib.qa_conv2d_3x3s2, pkg.ConvDesc()),
+                     (lib.qa_log_mel, pkg.MelDesc())):
         assert fn(None, ctypes.byref(desc)) == pkg.QA_EINVAL
         assert "null argument" in pkg.last_error()
 
@@ -126,6 +127,7 @@ def test_decoder_descriptor_layouts(pkg):
                "qa_layer_norm_desc": pkg.LayerNormDesc,
                "qa_window_attention_desc": pkg.WindowAttentionDesc,
                "qa_position_add_desc": pkg.PositionAddDesc, "qa_conv_desc": pkg.ConvDesc,
+               "qa_mel_desc": pkg.MelDesc,
                "qa_mlp_desc": pkg.MlpDesc}
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "qa.h"', "int main(void) {"]
     for cname, py in structs.items():
@@ -183,3 +185,11 @@ def test_errors_are_thread_local(pkg):
     t.join()
     assert "dtype" in seen["msg"]
     assert pkg.last_error() == main_msg
+
+
+def test_mel_filterbank_is_the_oracle_restatement(pkg, orc):
+    """qa_mel_filterbank (a host function of the C ABI) and the oracle's
+    restatement of create_mel_filterbank agree bit for bit."""
+    import numpy as np
+    assert np.array_equal(pkg.mel_filterbank(128, 400, 16000), orc.mel_filterbank(128, 400, 16000))
+    assert pkg.lib().qa_mel_filterbank(0, 400, 16000, None) == pkg.QA_EINVAL
