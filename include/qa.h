@@ -368,6 +368,55 @@ typedef struct qa_mel_desc {
 } qa_mel_desc;
 int qa_log_mel(qa_ctx* ctx, const qa_mel_desc* desc);
 
+/* RoPE tables for text positions 0..positions-1 (all three M-RoPE axes equal,
+ * as the aligner prefills them, src/mrope.rs:55-89 with text_positions):
+ * angle(p, j) = p / theta^(2j / hd) in f64, cos / sin [positions][hd] f32,
+ * the second half repeating the first.  Host function, no device needed. */
+int qa_rope_tables(int64_t positions, int hd, double theta, float* cos_out, float* sin_out);
+
+/* The decoder's input rows: out[r] = table[src[r]] (the token embedding) for
+ * src[r] >= 0 and audio[-src[r] - 1] (the audio tower's output row) for
+ * src[r] < 0 -- the host gather + scatter of align_raw_rows
+ * (src/align_inference.rs:688-714).  An index out of range gives a zero row.
+ * src is a device int32 array; hidden a multiple of 8; table, audio and out
+ * 16-byte aligned, in the 16-bit format of the decoder. */
+typedef struct qa_embed_desc {
+  uint32_t dtype;
+  uint32_t flags; /* reserved, must be 0 */
+  int64_t rows, hidden;
+  const int32_t* src;
+  const void* table;
+  int64_t vocab;
+  const void* audio;
+  int64_t n_audio;
+  void* out;
+} qa_embed_desc;
+int qa_embed_scatter(qa_ctx* ctx, const qa_embed_desc* desc);
+
+/* The timestamp head (src/align_inference.rs:738-805): for each of `rows`
+ * positions p (device int32), the final RMSNorm of h[p] in its folded form,
+ * x w / sqrt(sum (x w)^2 / n + eps), then logits = normed . score^T (f32) and
+ * classes = the first index of each row's largest logit (the caller
+ * multiplies by the segment time, 80 ms).  h [h_rows][ldh] in the 16-bit
+ * format; norm_w f32 [n]; score f32 [labels][n]; logits f32 [rows][labels]
+ * and classes int32 [rows] are device outputs.  A position out of range
+ * gives a zero row.  Uses the context's workspace (rows * n floats). */
+typedef struct qa_head_desc {
+  uint32_t dtype;
+  uint32_t flags; /* reserved, must be 0 */
+  int64_t rows;
+  const int32_t* positions;
+  const void* h;
+  int64_t h_rows, ldh, n;
+  const float* norm_w;
+  float eps;
+  const float* score;
+  int64_t labels;
+  float* logits;
+  int32_t* classes;
+} qa_head_desc;
+int qa_timestamp_head(qa_ctx* ctx, const qa_head_desc* desc);
+
 /* Message of the last failure on this thread ("" if none). */
 const char* qa_last_error(void);
 /* Library version string, e.g. "qa 0.1.0 (abi 1, gfx950)". */

@@ -106,6 +106,8 @@ def lib() -> ctypes.CDLL:
         L.or_stft_power.restype = None
         L.or_log_mel.argtypes = [p, i64, ci, p, p]
         L.or_log_mel.restype = None
+        L.or_timestamp_head.argtypes = [ci, i64, p, p, i64, i64, p, f, p, i64, p, p]
+        L.or_timestamp_head.restype = None
         L.or_vperm.restype = i64
         L.or_num_threads.restype = ctypes.c_int
         _lib = L
@@ -341,3 +343,18 @@ def log_mel(x: np.ndarray, filt: np.ndarray | None = None, n_mels: int = 128) ->
     out = np.empty((n_mels, x.size // 160), np.float32)
     lib().or_log_mel(_ptr(x), x.size, n_mels, _ptr(filt), _ptr(out))
     return out
+
+
+def timestamp_head(dtype: int, h: np.ndarray, positions, w: np.ndarray, eps: float,
+                   score: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """or_timestamp_head -> (logits f64 [rows, labels], classes int32 [rows])."""
+    h = _c(h, np.uint16)
+    pos = _c(np.asarray(positions), np.int32)
+    score = _c(score, np.float32)
+    labels, n = score.shape
+    logits = np.empty((pos.size, labels), np.float64)
+    cls = np.empty(pos.size, np.int32)
+    lib().or_timestamp_head(dtype, pos.size, _ptr(pos), _ptr(h), h.shape[1], n,
+                            _ptr(_c(w, np.float32)), ctypes.c_float(eps), _ptr(score), labels,
+                            _ptr(logits), _ptr(cls))
+    return logits, cls

@@ -140,6 +140,12 @@ void or_conv3x3s2(int dtype, int64_t batch, int64_t h, int64_t w, int64_t c_in, 
 void or_mel_filterbank(int n_mels, int n_fft, int sr, float* out);
 void or_stft_power(const float* x, int64_t n, int n_fft, int hop, double* power);
 void or_log_mel(const float* x, int64_t n, int n_mels, const float* filt, float* out);
+/* The timestamp head.  Pins (tests/test_oracle_head.py): the f64 closed form
+ * of the folded norm and the logits, and a constructed case whose argmax is
+ * known (score rows aligned with the normed rows, first index on ties). */
+void or_timestamp_head(int dtype, int64_t rows, const int32_t* pos, const uint16_t* h,
+                       int64_t ldh, int64_t n, const float* w, float eps, const float* score,
+                       int64_t labels, double* logits, int32_t* cls);
 
 #ifdef __cplusplus
 }

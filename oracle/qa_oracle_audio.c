@@ -260,3 +260,38 @@ void or_log_mel(const float* x, int64_t n, int n_mels, const float* filt, float*
   free(power);
   free(lm);
 }
+
+/* The timestamp head (src/align_inference.rs:738-805): for each position p,
+ * the folded final RMSNorm of h[p] in f32 (acc = sum (x w)^2 in order,
+ * inv = 1 / sqrt(acc / n + eps), y = x w inv), logits = y . score^T
+ * accumulated in f64 (the exact value the reference's f32 GEMM approximates),
+ * class = the first index of the largest logit.  logits f64 [rows][labels]. */
+void or_timestamp_head(int dtype, int64_t rows, const int32_t* pos, const uint16_t* h,
+                       int64_t ldh, int64_t n, const float* w, float eps, const float* score,
+                       int64_t labels, double* logits, int32_t* cls) {
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < rows; ++r) {
+    const uint16_t* x = h + (int64_t)pos[r] * ldh;
+    float acc = 0.f;
+    for (int64_t j = 0; j < n; ++j) {
+      const float v = or_h16_to_f32(x[j], dtype) * w[j];
+      acc += v * v;
+    }
+    const float inv = 1.0f / sqrtf(acc / (float)n + eps);
+    float* y = (float*)malloc(sizeof(float) * (size_t)n);
+    for (int64_t j = 0; j < n; ++j) y[j] = or_h16_to_f32(x[j], dtype) * w[j] * inv;
+    double best = -INFINITY;
+    int32_t bi = 0;
+    for (int64_t l = 0; l < labels; ++l) {
+      double s = 0.0;
+      for (int64_t j = 0; j < n; ++j) s += (double)y[j] * (double)score[l * n + j];
+      logits[r * labels + l] = s;
+      if (s > best) {
+        best = s;
+        bi = (int32_t)l;
+      }
+    }
+    cls[r] = bi;
+    free(y);
+  }
+}

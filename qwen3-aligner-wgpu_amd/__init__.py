@@ -234,13 +234,51 @@ class MelDesc(ctypes.Structure):
     ]
 
 
+class EmbedDesc(ctypes.Structure):
+    """qa_embed_desc (include/qa.h)."""
+
+    _fields_ = [
+        ("dtype", ctypes.c_uint32),
+        ("flags", ctypes.c_uint32),
+        ("rows", ctypes.c_int64),
+        ("hidden", ctypes.c_int64),
+        ("src", ctypes.c_void_p),
+        ("table", ctypes.c_void_p),
+        ("vocab", ctypes.c_int64),
+        ("audio", ctypes.c_void_p),
+        ("n_audio", ctypes.c_int64),
+        ("out", ctypes.c_void_p),
+    ]
+
+
+class HeadDesc(ctypes.Structure):
+    """qa_head_desc (include/qa.h)."""
+
+    _fields_ = [
+        ("dtype", ctypes.c_uint32),
+        ("flags", ctypes.c_uint32),
+        ("rows", ctypes.c_int64),
+        ("positions", ctypes.c_void_p),
+        ("h", ctypes.c_void_p),
+        ("h_rows", ctypes.c_int64),
+        ("ldh", ctypes.c_int64),
+        ("n", ctypes.c_int64),
+        ("norm_w", ctypes.c_void_p),
+        ("eps", ctypes.c_float),
+        ("score", ctypes.c_void_p),
+        ("labels", ctypes.c_int64),
+        ("logits", ctypes.c_void_p),
+        ("classes", ctypes.c_void_p),
+    ]
+
+
 # Every symbol include/qa.h declares (checked by tests/test_abi.py).
 EXPORTS = (
     "qa_ctx_create", "qa_ctx_destroy", "qa_ctx_stream", "qa_alloc", "qa_free",
     "qa_upload", "qa_download", "qa_sync", "qa_linear", "qa_linear_validate",
     "qa_mlp_fused", "qa_rms_norm", "qa_qk_norm_rope", "qa_attention_prefill",
     "qa_layer_norm", "qa_window_attention", "qa_add_position_table", "qa_conv2d_3x3s2",
-    "qa_mel_filterbank", "qa_log_mel",
+    "qa_mel_filterbank", "qa_log_mel", "qa_rope_tables", "qa_embed_scatter", "qa_timestamp_head",
     "qa_last_error", "qa_version",
 )
 
@@ -277,6 +315,9 @@ def lib() -> ctypes.CDLL:
         L.qa_conv2d_3x3s2.argtypes = [vp, ctypes.POINTER(ConvDesc)]
         L.qa_mel_filterbank.argtypes = [i, i, i, vp]
         L.qa_log_mel.argtypes = [vp, ctypes.POINTER(MelDesc)]
+        L.qa_rope_tables.argtypes = [ctypes.c_int64, i, ctypes.c_double, vp, vp]
+        L.qa_embed_scatter.argtypes = [vp, ctypes.POINTER(EmbedDesc)]
+        L.qa_timestamp_head.argtypes = [vp, ctypes.POINTER(HeadDesc)]
         L.qa_last_error.restype = ctypes.c_char_p
         L.qa_version.restype = ctypes.c_char_p
         for name in EXPORTS:
@@ -403,12 +444,26 @@ class Context:
     def log_mel(self, desc: MelDesc) -> None:
         check(lib().qa_log_mel(self.handle, ctypes.byref(desc)))
 
+    def embed_scatter(self, desc: EmbedDesc) -> None:
+        check(lib().qa_embed_scatter(self.handle, ctypes.byref(desc)))
+
+    def timestamp_head(self, desc: HeadDesc) -> None:
+        check(lib().qa_timestamp_head(self.handle, ctypes.byref(desc)))
+
 
 def mel_filterbank(n_mels: int = 128, n_fft: int = 400, sample_rate: int = 16000) -> np.ndarray:
     """qa_mel_filterbank (host): the slaney filterbank [n_mels, n_fft // 2 + 1] f32."""
     out = np.empty((n_mels, n_fft // 2 + 1), np.float32)
     check(lib().qa_mel_filterbank(n_mels, n_fft, sample_rate, out.ctypes.data))
     return out
+
+
+def rope_tables(positions: int, hd: int = 128, theta: float = 1e6) -> tuple[np.ndarray, np.ndarray]:
+    """qa_rope_tables (host): cos, sin [positions, hd] f32 for text positions."""
+    c = np.empty((positions, hd), np.float32)
+    s = np.empty((positions, hd), np.float32)
+    check(lib().qa_rope_tables(positions, hd, theta, c.ctypes.data, s.ctypes.data))
+    return c, s
 
 
 def linear_desc(dtype: int, m: int, n: int, k: int, a, w, c, *, flags: int = 0, bias=None,

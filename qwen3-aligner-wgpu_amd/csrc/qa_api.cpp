@@ -734,6 +734,85 @@ int qa_log_mel(qa_ctx* ctx, const qa_mel_desc* d) {
   return e == hipSuccess ? ok() : hip_fail(e, "qa_log_mel launch");
 }
 
+int qa_rope_tables(int64_t positions, int hd, double theta, float* cos_out, float* sin_out) {
+  if (positions <= 0 || hd <= 0 || hd % 2 || !(theta > 0.0) || !cos_out || !sin_out)
+    return fail(QA_EINVAL, "qa_rope_tables: bad argument");
+  const int half = hd / 2;
+  std::vector<double> inv((size_t)half);
+  for (int j = 0; j < half; ++j) inv[(size_t)j] = 1.0 / std::pow(theta, 2.0 * j / hd);
+  for (int64_t p = 0; p < positions; ++p)
+    for (int j = 0; j < half; ++j) {
+      const double a = (double)p * inv[(size_t)j];
+      const float c = (float)std::cos(a), s = (float)std::sin(a);
+      cos_out[p * hd + j] = cos_out[p * hd + j + half] = c;
+      sin_out[p * hd + j] = sin_out[p * hd + j + half] = s;
+    }
+  return ok();
+}
+
+int qa_embed_scatter(qa_ctx* ctx, const qa_embed_desc* d) {
+  if (!ctx || !d) return fail(QA_EINVAL, "qa_embed_scatter: null argument");
+  if (d->dtype != QA_F16 && d->dtype != QA_BF16)
+    return fail(QA_EINVAL, "qa_embed_scatter: dtype %u is neither QA_F16 nor QA_BF16", d->dtype);
+  if (d->flags) return fail(QA_EINVAL, "qa_embed_scatter: flags must be 0");
+  if (d->rows < 0 || d->hidden <= 0 || d->hidden % 8 || d->hidden > kI32 || d->vocab < 0 ||
+      d->n_audio < 0)
+    return fail(QA_EINVAL, "qa_embed_scatter: bad shape");
+  if (!d->src || !d->out || (d->vocab && !d->table) || (d->n_audio && !d->audio))
+    return fail(QA_EINVAL, "qa_embed_scatter: null pointer");
+  if (!aligned(d->out, 16) || (d->table && !aligned(d->table, 16)) ||
+      (d->audio && !aligned(d->audio, 16)) || !aligned(d->src, 4))
+    return fail(QA_EINVAL, "qa_embed_scatter: table, audio and out must be 16-byte aligned");
+  if (d->rows == 0) return ok();
+  if (int rc = set_device(ctx)) return rc;
+  qa::EmbedParams p{};
+  p.src = d->src;
+  p.table = (const uint16_t*)d->table;
+  p.audio = (const uint16_t*)d->audio;
+  p.out = (uint16_t*)d->out;
+  p.rows = d->rows;
+  p.vocab = d->vocab;
+  p.n_audio = d->n_audio;
+  p.hidden = (int)d->hidden;
+  const hipError_t e = qa::launch_embed_scatter(p, ctx->stream);
+  return e == hipSuccess ? ok() : hip_fail(e, "qa_embed_scatter launch");
+}
+
+int qa_timestamp_head(qa_ctx* ctx, const qa_head_desc* d) {
+  if (!ctx || !d) return fail(QA_EINVAL, "qa_timestamp_head: null argument");
+  if (d->dtype != QA_F16 && d->dtype != QA_BF16)
+    return fail(QA_EINVAL, "qa_timestamp_head: dtype %u is neither QA_F16 nor QA_BF16", d->dtype);
+  if (d->flags) return fail(QA_EINVAL, "qa_timestamp_head: flags must be 0");
+  if (d->rows < 0 || d->n <= 0 || d->n > kI32 || d->labels <= 0 || d->labels > kI32 ||
+      d->h_rows < 0 || d->ldh < d->n || (d->rows + 31) / 32 > 65535)
+    return fail(QA_EINVAL, "qa_timestamp_head: bad shape");
+  if (!d->positions || !d->h || !d->norm_w || !d->score || !d->logits || !d->classes)
+    return fail(QA_EINVAL, "qa_timestamp_head: null pointer");
+  if (!aligned(d->h, 2) || !aligned(d->norm_w, 4) || !aligned(d->score, 4) ||
+      !aligned(d->logits, 4) || !aligned(d->classes, 4) || !aligned(d->positions, 4))
+    return fail(QA_EINVAL, "qa_timestamp_head: misaligned pointer");
+  if (!(d->eps >= 0.0f)) return fail(QA_EINVAL, "qa_timestamp_head: eps must be >= 0");
+  if (d->rows == 0) return ok();
+  if (int rc = set_device(ctx)) return rc;
+  if (int rc = ensure_workspace(ctx, (size_t)(d->rows * d->n))) return rc;
+  qa::HeadParams p{};
+  p.pos = d->positions;
+  p.h = (const uint16_t*)d->h;
+  p.w = d->norm_w;
+  p.score = d->score;
+  p.normed = ctx->ws;
+  p.logits = d->logits;
+  p.cls = d->classes;
+  p.rows = d->rows;
+  p.h_rows = d->h_rows;
+  p.ldh = d->ldh;
+  p.labels = d->labels;
+  p.n = (int)d->n;
+  p.eps = d->eps;
+  const hipError_t e = qa::launch_timestamp_head((int)d->dtype, p, ctx->stream);
+  return e == hipSuccess ? ok() : hip_fail(e, "qa_timestamp_head launch");
+}
+
 int qa_layer_norm(qa_ctx* ctx, const qa_layer_norm_desc* d) {
   if (!ctx || !d) return fail(QA_EINVAL, "qa_layer_norm: null argument");
   if (d->dtype != QA_F16 && d->dtype != QA_BF16)

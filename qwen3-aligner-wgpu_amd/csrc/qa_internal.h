@@ -175,6 +175,30 @@ struct MelParams {
 };
 hipError_t launch_log_mel(int dtype, const MelParams& p, hipStream_t stream);
 
+// The aligner's input rows and timestamp head (qa_head.hip).
+struct EmbedParams {
+  const int32_t* src;
+  const uint16_t* table;
+  const uint16_t* audio;
+  uint16_t* out;
+  int64_t rows, vocab, n_audio;
+  int hidden;
+};
+hipError_t launch_embed_scatter(const EmbedParams& p, hipStream_t stream);
+struct HeadParams {
+  const int32_t* pos;
+  const uint16_t* h;
+  const float* w;
+  const float* score;
+  float* normed;  // workspace [rows][n]
+  float* logits;  // [rows][labels]
+  int32_t* cls;   // [rows]
+  int64_t rows, h_rows, ldh, labels;
+  int n;
+  float eps;
+};
+hipError_t launch_timestamp_head(int dtype, const HeadParams& p, hipStream_t stream);
+
 // p16: probabilities rounded once to the 16-bit format (else two 16-bit terms).
 hipError_t launch_attention(int dtype, const AttnParams& p, bool p16, hipStream_t stream);
 

@@ -110,7 +110,9 @@ def test_calls_without_context_fail_cleanly(pkg):
                      (lib.qa_window_attention, pkg.WindowAttentionDesc()),
                      (lib.qa_add_position_table, pkg.PositionAddDesc()),
                      (lib.qa_conv2d_3x3s2, pkg.ConvDesc()),
-                     (lib.qa_log_mel, pkg.MelDesc())):
+                     (lib.qa_log_mel, pkg.MelDesc()),
+                     (lib.qa_embed_scatter, pkg.EmbedDesc()),
+                     (lib.qa_timestamp_head, pkg.HeadDesc())):
         assert fn(None, ctypes.byref(desc)) == pkg.QA_EINVAL
         assert "null argument" in pkg.last_error()
 
@@ -127,7 +129,8 @@ def test_decoder_descriptor_layouts(pkg):
                "qa_layer_norm_desc": pkg.LayerNormDesc,
                "qa_window_attention_desc": pkg.WindowAttentionDesc,
                "qa_position_add_desc": pkg.PositionAddDesc, "qa_conv_desc": pkg.ConvDesc,
-               "qa_mel_desc": pkg.MelDesc,
+               "qa_mel_desc": pkg.MelDesc, "qa_embed_desc": pkg.EmbedDesc,
+               "qa_head_desc": pkg.HeadDesc,
                "qa_mlp_desc": pkg.MlpDesc}
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "qa.h"', "int main(void) {"]
     for cname, py in structs.items():
@@ -193,3 +196,13 @@ def test_mel_filterbank_is_the_oracle_restatement(pkg, orc):
     import numpy as np
     assert np.array_equal(pkg.mel_filterbank(128, 400, 16000), orc.mel_filterbank(128, 400, 16000))
     assert pkg.lib().qa_mel_filterbank(0, 400, 16000, None) == pkg.QA_EINVAL
+
+
+def test_rope_tables_match_the_text_position_definition(pkg):
+    """qa_rope_tables (host) equals the closed form angle = p / theta^(2j/hd)
+    with repeated halves (src/mrope.rs:55-89 for text positions)."""
+    import numpy as np
+    from conftest import rope_tables
+    c, s = pkg.rope_tables(300, 128, 1e6)
+    wc, ws = rope_tables(300, 128, 0, theta=1e6)
+    assert np.array_equal(c, wc) and np.array_equal(s, ws)
