@@ -221,6 +221,62 @@ def bench_audio_tower(host, ctx, dtype, warmup, steps):
     }
 
 
+E2E = dict(seconds=300.0, words=120, enc_layers=18, dec_layers=28, dtype=0, seed=5)
+E2E_GOLDEN = os.path.join(ROOT, "tests", "golden", "e2e_300s.json")
+
+
+def bench_e2e(pkg, ctx, warmup, steps):
+    """the whole aligner forward over 300 s of synthetic
+    audio and 120 synthetic words, f16, random-init 0.6B-shaped weights:
+    log-mel -> 18-layer audio tower -> embedding gather + audio scatter ->
+    28-layer decoder prefill -> timestamp head, one hipGraph per step with
+    the samples and the assembled input resident in HBM.  Also times the
+    eager forward with the classes' readback and the host repair, and
+    compares the classes with the oracle's (the committed fixture made from
+    the same seeded inputs by tests/golden/make_e2e_golden.py)."""
+    from qwen3_aligner_wgpu_amd import synthetic as syn
+    c = E2E
+    w = syn.aligner_weights(c["dtype"], c["enc_layers"], c["dec_layers"], c["seed"])
+    x = syn.synthetic_audio(c["seconds"], c["seed"])
+    words = [syn.word_token_ids(t) for t in syn.synthetic_words(c["words"], c["seed"])]
+    al, enc, dec = syn.build_aligner(pkg, ctx, c["dtype"], w, c["seconds"] + 0.01, max(PREFILL_ROWS))
+    del w
+    try:
+        info = al.prepare(x, words)
+        ev_ms, wall_ms = al.time(warmup, steps, use_graph=True)
+        phases = al.profile(2)
+        t0 = time.perf_counter()
+        reps = 3
+        for _ in range(reps):
+            al.forward()
+            al.result()
+        eager_ms = (time.perf_counter() - t0) * 1e3 / reps
+        classes = al.read("classes")
+    finally:
+        al.close()
+        enc.close()
+        dec.close()
+    out = {
+        "ms": round(max(ev_ms, wall_ms), 3),
+        "event_ms": round(ev_ms, 3),
+        "wall_ms": round(wall_ms, 3),
+        "eager_with_readback_ms": round(eager_ms, 3),
+        "phase_ms": {k: round(v, 3) for k, v in phases.items()},
+        "seq": info["seq"], "audio_tokens": info["n_audio"], "slots": info["slots"],
+    }
+    try:
+        gold = json.load(open(E2E_GOLDEN))
+        if gold["config"] == c:
+            want = np.array(gold["classes"])
+            clear = np.array(gold["gap"]) > 2.0 ** -8 * np.array(gold["logit_rms"])
+            out["argmax_identical_slots"] = int((classes == want).sum())
+            out["argmax_clear_margin_slots"] = int(clear.sum())
+            out["argmax_identical_at_clear_slots"] = bool((classes == want)[clear].all())
+    except (OSError, KeyError, ValueError):
+        out["argmax_identical_slots"] = None
+    return out
+
+
 def bench_encoder(pkg, host, ctx, m, warmup, steps):
     dt = pkg.BF16
     d, f, ck = ENC["d_model"], ENC["ffn"], ENC["conv_k"]
@@ -336,6 +392,9 @@ def main():
         r = bench_audio_tower(host, ctx, pkg.F16, 1, 3)
         detail["audio_tower_300s"] = r
         log(f"[bench] audio tower 300 s: {r}")
+    e2e = bench_e2e(pkg, ctx, 2, 5)
+    detail["e2e_300s"] = e2e
+    log(f"[bench] aligner forward 300 s: {e2e}")
     ctx.close()
 
     traffic, traffic_kernel = measured_traffic("gu")
@@ -369,6 +428,7 @@ def main():
             "gflop_per_step": round(total_flops / 1e9, 2),
         },
         "pct_mfma_peak": round(100 * value / PEAK_F16_TFLOPS, 2),
+        "e2e_ms_per_300s_audio": e2e["ms"],
         "roofline": {
             "bound": "mfma",
             "kernel": "gate|up GEMM + SiLU.up epilogue, [1024,1024]x[6144,1024]^T",

@@ -358,3 +358,52 @@ def timestamp_head(dtype: int, h: np.ndarray, positions, w: np.ndarray, eps: flo
                             _ptr(_c(w, np.float32)), ctypes.c_float(eps), _ptr(score), labels,
                             _ptr(logits), _ptr(cls))
     return logits, cls
+
+
+def fix_timestamps(data) -> list[int]:
+    """The timestamp repair, restated from src/postprocess.rs:33-111 (test
+    infrastructure: the checker of the host library's qah_fix_timestamps).
+
+    best[i] is the longest non-decreasing subsequence ending at i, prev[i]
+    the earliest predecessor reaching it; the subsequence kept ends at the
+    first i of maximal length.  Every maximal run of other positions is
+    rewritten from its kept neighbours: runs of 1-2 take the neighbour nearer
+    by index (left when equally near), longer runs the linear interpolation
+    left + (right - left) / (len + 1) * k truncated toward zero, and a run
+    with a single neighbour takes that neighbour's value."""
+    data = [int(v) for v in data]
+    n = len(data)
+    if n == 0:
+        return []
+    best, prev = [1] * n, [-1] * n
+    for i in range(n):
+        for j in range(i):
+            if data[j] <= data[i] and best[j] + 1 > best[i]:
+                best[i], prev[i] = best[j] + 1, j
+    i = best.index(max(best))
+    keep = set()
+    while i != -1:
+        keep.add(i)
+        i = prev[i]
+    out = list(data)
+    i = 0
+    while i < n:
+        if i in keep:
+            i += 1
+            continue
+        j = i
+        while j < n and j not in keep:
+            j += 1
+        left = out[i - 1] if i > 0 else None
+        right = out[j] if j < n else None
+        run = j - i
+        for p in range(i, j):
+            if left is not None and right is not None:
+                if run <= 2:
+                    out[p] = left if p - (i - 1) <= j - p else right
+                else:
+                    out[p] = int(left + (right - left) / (run + 1) * (p - i + 1))
+            else:
+                out[p] = left if left is not None else right
+        i = j
+    return out

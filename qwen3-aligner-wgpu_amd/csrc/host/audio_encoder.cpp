@@ -17,6 +17,7 @@
 #include <cmath>
 #include <cstring>
 
+#include "handles.hpp"
 #include "qa_host.h"
 #include "timing.hpp"
 
@@ -311,9 +312,6 @@ int AudioEncoder::read(int which, int64_t rows, uint16_t* host) {
 // C surface
 using namespace qa_host;
 
-struct qah_aenc {
-  AudioEncoder* e;
-};
 
 extern "C" {
 

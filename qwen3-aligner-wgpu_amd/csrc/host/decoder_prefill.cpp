@@ -16,6 +16,7 @@
 #include <algorithm>
 #include <cstring>
 
+#include "handles.hpp"
 #include "qa_host.h"
 #include "timing.hpp"
 
@@ -217,9 +218,6 @@ int TextDecoder::read(int which, int rows, uint16_t* host) {
 // C surface
 using namespace qa_host;
 
-struct qah_tdec {
-  TextDecoder* d;
-};
 
 extern "C" {
 

@@ -188,6 +188,40 @@ int qah_aenc_time(qah_aenc* a, int n_chunks, int tail_frames, int warmup, int st
 int qah_aenc_profile(qah_aenc* a, int n_chunks, int tail_frames, int steps, double* ms);
 void qah_aenc_destroy(qah_aenc* a);
 
+/* The aligner's forward pass (Aligner::align_raw_rows,
+ * src/align_inference.rs:646-805): samples -> log-mel -> the encoder `enc`
+ * -> embedding gather + audio scatter -> the decoder `dec` -> timestamp head,
+ * then fix_timestamps on the host.  enc and dec stay owned by the caller and
+ * must outlive the aligner. */
+typedef struct qah_aligner qah_aligner;
+/* The timestamp repair alone (src/postprocess.rs:33-111); out may not alias data. */
+void qah_fix_timestamps(const int64_t* data, int64_t n, int64_t* out);
+int qah_aligner_create(qa_ctx* ctx, qah_aenc* enc, qah_tdec* dec, int64_t vocab, int64_t labels,
+                       double segment_ms, int64_t max_samples, qah_aligner** out);
+/* Token embedding [vocab][hidden] in the decoder's 16-bit format. */
+int qah_aligner_load_embed(qah_aligner* h, const uint16_t* table);
+/* Final RMSNorm weight f32 [hidden] and score head f32 [labels][hidden]. */
+int qah_aligner_load_head(qah_aligner* h, const float* norm_w, const float* score);
+/* Assemble and upload one input: f32 samples at 16 kHz, and n_words words
+ * given as token ids (word_lens[w] ids each, concatenated in word_ids).
+ * info (optional, 5 entries): sequence length, audio tokens, timestamp
+ * slots, mel chunks, frames in the last chunk (0 = full). */
+int qah_aligner_prepare(qah_aligner* h, const float* samples, int64_t n_samples, int n_words,
+                        const int32_t* word_lens, const int32_t* word_ids, int64_t* info);
+/* Enqueue the device pass (no wait). */
+int qah_aligner_forward(qah_aligner* h);
+/* Classes -> raw ms (class x segment) and repaired ms, 2 per word. */
+int qah_aligner_result(qah_aligner* h, int64_t* raw_ms, int64_t* fixed_ms);
+/* which = 0 classes int32 [slots], 1 logits f32 [slots][labels], 2 input ids
+ * int32 [seq], 3 timestamp positions int32 [slots], 4 row sources int32
+ * [seq] (token id, or -1 - k for audio row k). */
+int qah_aligner_read(qah_aligner* h, int which, void* host);
+int qah_aligner_time(qah_aligner* h, int warmup, int steps, int use_graph, double* ms_per_step,
+                     double* wall_ms_per_step);
+/* Event-bracketed ms over `steps` forwards: mel, tower, scatter, prefill, head. */
+int qah_aligner_profile(qah_aligner* h, int steps, double* ms);
+void qah_aligner_destroy(qah_aligner* h);
+
 /* Time `iters` back-to-back launches of one descriptor (HIP events around the
  * whole run on the context's stream); ms per launch. */
 int qah_time_linear(qa_ctx* ctx, const qa_linear_desc* desc, int warmup, int iters,

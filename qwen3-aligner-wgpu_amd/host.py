@@ -72,6 +72,20 @@ def declare(L: ctypes.CDLL) -> None:
     L.qah_aenc_destroy.argtypes = [_vp]
     L.qah_aenc_destroy.restype = None
     del _fp
+    L.qah_fix_timestamps.argtypes = [_vp, ctypes.c_int64, _vp]
+    L.qah_fix_timestamps.restype = None
+    L.qah_aligner_create.argtypes = [_vp, _vp, _vp, ctypes.c_int64, ctypes.c_int64,
+                                     ctypes.c_double, ctypes.c_int64, ctypes.POINTER(_vp)]
+    L.qah_aligner_load_embed.argtypes = [_vp, _vp]
+    L.qah_aligner_load_head.argtypes = [_vp, _vp, _vp]
+    L.qah_aligner_prepare.argtypes = [_vp, _vp, ctypes.c_int64, _i, _vp, _vp, _vp]
+    L.qah_aligner_forward.argtypes = [_vp]
+    L.qah_aligner_result.argtypes = [_vp, _vp, _vp]
+    L.qah_aligner_read.argtypes = [_vp, _i, _vp]
+    L.qah_aligner_time.argtypes = [_vp, _i, _i, _i, _dp, _dp]
+    L.qah_aligner_profile.argtypes = [_vp, _i, _dp]
+    L.qah_aligner_destroy.argtypes = [_vp]
+    L.qah_aligner_destroy.restype = None
     L.qah_time_linear.argtypes = [_vp, _vp, _i, _i, _dp]
     L.qah_copy_calibration.argtypes = [_vp, _sz, _i]
     for name in ("qah_decoder_create", "qah_decoder_load_layer", "qah_decoder_set_inputs",
@@ -384,6 +398,87 @@ class AudioEncoder:
         out = (ctypes.c_double * 12)()
         check(host_lib().qah_aenc_profile(self.handle, n_chunks, tail_frames, steps, out))
         return dict(zip(self.PROFILE, list(out)))
+
+
+def fix_timestamps(data) -> np.ndarray:
+    """qah_fix_timestamps: the timestamp repair (src/postprocess.rs:33-111)."""
+    data = np.ascontiguousarray(data, np.int64)
+    out = np.empty_like(data)
+    host_lib().qah_fix_timestamps(_p(data), data.size, _p(out))
+    return out
+
+
+class Aligner:
+    """qah_aligner: the aligner's forward pass over an AudioEncoder and a
+    TextDecoder (Aligner::align_raw_rows, src/align_inference.rs:646-805)."""
+
+    PHASES = ("mel", "tower", "scatter", "prefill", "head")
+
+    def __init__(self, ctx, enc: AudioEncoder, dec: TextDecoder, vocab: int = 151936,
+                 labels: int = 5000, segment_ms: float = 80.0, max_samples: int = 300 * 16000):
+        self.ctx, self.enc, self.dec, self.vocab, self.labels = ctx, enc, dec, vocab, labels
+        h = _vp()
+        check(host_lib().qah_aligner_create(ctx.handle, enc.handle, dec.handle, vocab, labels,
+                                            segment_ms, max_samples, ctypes.byref(h)))
+        self.handle = h.value
+        self.info = None
+
+    def close(self):
+        if self.handle:
+            host_lib().qah_aligner_destroy(self.handle)
+            self.handle = None
+
+    def load_embed(self, table):
+        table = np.ascontiguousarray(table, np.uint16)
+        assert table.shape == (self.vocab, self.dec.hidden)
+        check(host_lib().qah_aligner_load_embed(self.handle, _p(table)))
+
+    def load_head(self, norm_w, score):
+        norm_w = np.ascontiguousarray(norm_w, np.float32)
+        score = np.ascontiguousarray(score, np.float32)
+        assert norm_w.shape == (self.dec.hidden,) and score.shape == (self.labels, self.dec.hidden)
+        check(host_lib().qah_aligner_load_head(self.handle, _p(norm_w), _p(score)))
+
+    def prepare(self, samples, words) -> dict:
+        """words: a list of token-id lists, one per word."""
+        samples = np.ascontiguousarray(samples, np.float32)
+        lens = np.array([len(w) for w in words], np.int32)
+        ids = np.array([i for w in words for i in w] or [0], np.int32)
+        info = np.zeros(5, np.int64)
+        check(host_lib().qah_aligner_prepare(self.handle, _p(samples), samples.size, len(words),
+                                             _p(lens), _p(ids), _p(info)))
+        self.info = dict(zip(("seq", "n_audio", "slots", "chunks", "tail"), map(int, info)))
+        return self.info
+
+    def forward(self):
+        check(host_lib().qah_aligner_forward(self.handle))
+
+    def result(self) -> tuple[np.ndarray, np.ndarray]:
+        raw = np.zeros(self.info["slots"], np.int64)
+        fixed = np.zeros_like(raw)
+        check(host_lib().qah_aligner_result(self.handle, _p(raw), _p(fixed)))
+        return raw, fixed
+
+    def read(self, which: str) -> np.ndarray:
+        n, seq = self.info["slots"], self.info["seq"]
+        idx, shape, dt = {"classes": (0, (n,), np.int32),
+                          "logits": (1, (n, self.labels), np.float32),
+                          "ids": (2, (seq,), np.int32), "ts_pos": (3, (n,), np.int32),
+                          "src": (4, (seq,), np.int32)}[which]
+        out = np.empty(shape, dt)
+        check(host_lib().qah_aligner_read(self.handle, idx, out.ctypes.data))
+        return out
+
+    def time(self, warmup, steps, use_graph=True) -> tuple[float, float]:
+        ms, wall = ctypes.c_double(), ctypes.c_double()
+        check(host_lib().qah_aligner_time(self.handle, warmup, steps, int(use_graph),
+                                          ctypes.byref(ms), ctypes.byref(wall)))
+        return ms.value, wall.value
+
+    def profile(self, steps) -> dict:
+        out = (ctypes.c_double * 5)()
+        check(host_lib().qah_aligner_profile(self.handle, steps, out))
+        return dict(zip(self.PHASES, list(out)))
 
 
 def time_linear(ctx, desc, warmup: int, iters: int) -> float:

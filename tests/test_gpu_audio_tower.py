@@ -26,6 +26,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
+from chains import oracle_tower as _oracle_tower, perm_co as _perm_co, perm_conv as _perm_conv
 from conftest import assert_parity, ulp16
 
 pytestmark = pytest.mark.gpu
@@ -72,48 +73,6 @@ def _build(ctx, dtype, w, n_chunks):
     (lw, lb), (p1w, p1b), (p2w, p2b) = w["post"]
     enc.load_post(lw, lb, p1w, p1b, p2w, p2b)
     return enc
-
-
-def _perm_conv(w):
-    """[c_out][c_in][3][3] -> [c_out][ldw] in (kh, kw, ic) order (zero-padded)."""
-    c_out, c_in = w.shape[:2]
-    ldw = (9 * c_in + 7) // 8 * 8
-    out = np.zeros((c_out, ldw), np.uint16)
-    out[:, :9 * c_in] = w.transpose(0, 2, 3, 1).reshape(c_out, 9 * c_in)
-    return out
-
-
-def _perm_co(w):
-    """conv_out columns (c, f) -> (f, c)."""
-    return np.ascontiguousarray(w.reshape(DM, CC, 16).transpose(0, 2, 1).reshape(DM, CC * 16))
-
-
-def _oracle_tower(orc, dtype, w, mel, n_tok, start="mel", h0=None):
-    if start == "mel":
-        b = mel.shape[0]
-        x = mel.reshape(b, NM, CS, 1)
-        y1 = orc.conv3x3s2(dtype, x, _perm_conv(w["conv"][0][0]), w["conv"][0][1])
-        y2 = orc.conv3x3s2(dtype, y1.reshape(b, 64, 50, CC), _perm_conv(w["conv"][1][0]), w["conv"][1][1])
-        y3 = orc.conv3x3s2(dtype, y2.reshape(b, 32, 25, CC), _perm_conv(w["conv"][2][0]), w["conv"][2][1],
-                           token_major=True).reshape(b * 13, CC * 16)[:n_tok]
-        h = orc.linear(dtype, np.ascontiguousarray(y3), _perm_co(w["co"][0]),
-                       np.zeros((n_tok, DM), np.uint16), bias=w["co"][1])
-        h = orc.add_position_table(dtype, h, orc.sinusoid_table(13, DM))
-    else:
-        h = h0
-    for l in w["layers"]:
-        x = orc.layer_norm(dtype, h, *l["ln1"], 1e-5)
-        qkv = orc.linear(dtype, x, l["qkv"][0], np.zeros((n_tok, 3 * DM), np.uint16), bias=l["qkv"][1])
-        a = orc.window_attention(dtype, qkv, NH, 64, WLEN)
-        h = orc.linear(dtype, a, l["o"][0], h.copy(), flags=orc.ACCUMULATE, bias=l["o"][1])
-        x = orc.layer_norm(dtype, h, *l["ln2"], 1e-5)
-        act = orc.linear(dtype, x, l["fc1"][0], np.zeros((n_tok, FFN), np.uint16),
-                         flags=orc.EPI_GELU, bias=l["fc1"][1])
-        h = orc.linear(dtype, act, l["fc2"][0], h.copy(), flags=orc.ACCUMULATE, bias=l["fc2"][1])
-    (lw, lb), (p1w, p1b), (p2w, p2b) = w["post"]
-    x = orc.layer_norm(dtype, h, lw, lb, 1e-5)
-    pa = orc.linear(dtype, x, p1w, np.zeros((n_tok, DM), np.uint16), flags=orc.EPI_GELU, bias=p1b)
-    return orc.linear(dtype, pa, p2w, np.zeros((n_tok, OD), np.uint16), bias=p2b), h
 
 
 @pytest.mark.parametrize("dtype", [F16, BF16], ids=["f16", "bf16"])

