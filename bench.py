@@ -306,6 +306,8 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=12.0,
                     help="seconds of oracle work for cpu_baseline (0 disables)")
     ap.add_argument("--no-detail", action="store_true", help="skip configs 1, 2, 4")
+    ap.add_argument("--e2e-only", action="store_true",
+                    help="only the config-5 aligner forward (for profiling); prints its detail")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 512 MiB copy 3 times (calibrates FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
@@ -324,6 +326,11 @@ def main():
         with pkg.Context(0) as ctx:
             host.copy_calibration(ctx, COPY_CAL_BYTES, 3)
         log(f"[bench] copied {COPY_CAL_BYTES} bytes x3")
+        return
+
+    if args.e2e_only:
+        with pkg.Context(0) as ctx:
+            print(json.dumps({"e2e_300s": bench_e2e(pkg, ctx, args.warmup, args.steps)}), flush=True)
         return
 
     m = 1024
