@@ -109,6 +109,97 @@ __global__ void __launch_bounds__(256) qk_norm_rope_kernel(const RopeParams p) {
   }
 }
 
+// The same op with 16-byte accesses, for hd in {64, 128, 256} and 16-byte
+// aligned rows: one wave per (row, group of 1024 / hd head slots), hd / 16
+// lanes per head.  A lane owns the 8-element chunks c and c + hd / 16 of its
+// head, i.e. the rotate-half partners j and j + hd / 2 for the 8 j of chunk
+// c, and the head's sum of squares is reduced over its hd / 16 lanes.  The
+// arithmetic per element is qk_norm_rope_kernel's; only the order of the
+// sum of squares differs.
+template <int DT>
+__global__ void __launch_bounds__(256) qk_norm_rope_vec_kernel(const RopeParams p) {
+  const int lane = threadIdx.x & 63;
+  const int L = p.hd >> 4;  // lanes per head: 4, 8 or 16
+  const int hpw = 64 / L;   // head slots per wave
+  const int slots = p.nqh + p.nkvh;
+  const int groups = (slots + hpw - 1) / hpw;
+  const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (item >= p.rows * groups) return;
+  const int64_t r = item / groups;
+  const int slot = (int)(item % groups) * hpw + lane / L;
+  const int c = lane % L;
+  const bool active = slot < slots;
+  const int half = p.hd >> 1;
+  const bool is_q = slot < p.nqh;
+  const int head = is_q ? slot : slot - p.nqh;
+  // q heads then k heads are contiguous at the start of the fused row
+  const uint16_t* raw = p.qkv + r * p.ldqkv + (int64_t)(active ? slot : 0) * p.hd;
+  u32x4 va = {0, 0, 0, 0}, vb = {0, 0, 0, 0};
+  if (active) {
+    va = *reinterpret_cast<const u32x4*>(raw + 8 * c);
+    vb = *reinterpret_cast<const u32x4*>(raw + half + 8 * c);
+  }
+  float xa[8], xb[8];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    xa[2 * e] = widen16<DT>(va[e] & 0xffffu);
+    xa[2 * e + 1] = widen16<DT>(va[e] >> 16);
+    xb[2 * e] = widen16<DT>(vb[e] & 0xffffu);
+    xb[2 * e + 1] = widen16<DT>(vb[e] >> 16);
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    s += xa[e] * xa[e];
+    s += xb[e] * xb[e];
+  }
+  for (int o = 1; o < L; o <<= 1) s += __shfl_xor(s, o, 64);
+  if (!active) return;
+  const float inv = 1.0f / sqrtf(s / (float)p.hd + p.eps);
+  const float* nw = is_q ? p.qn : p.kn;
+  const float* cs = p.cos + (p.pos0 + r) * p.hd;
+  const float* sn = p.sin + (p.pos0 + r) * p.hd;
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  float wa[8], wb[8], ca[8], cb[8], sa[8], sb[8];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const f32x4 w0 = *reinterpret_cast<const f32x4*>(nw + 8 * c + 4 * h);
+    const f32x4 w1 = *reinterpret_cast<const f32x4*>(nw + half + 8 * c + 4 * h);
+    const f32x4 c0 = *reinterpret_cast<const f32x4*>(cs + 8 * c + 4 * h);
+    const f32x4 c1 = *reinterpret_cast<const f32x4*>(cs + half + 8 * c + 4 * h);
+    const f32x4 s0 = *reinterpret_cast<const f32x4*>(sn + 8 * c + 4 * h);
+    const f32x4 s1 = *reinterpret_cast<const f32x4*>(sn + half + 8 * c + 4 * h);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      wa[4 * h + e] = w0[e];
+      wb[4 * h + e] = w1[e];
+      ca[4 * h + e] = c0[e];
+      cb[4 * h + e] = c1[e];
+      sa[4 * h + e] = s0[e];
+      sb[4 * h + e] = s1[e];
+    }
+  }
+  u32x4 oa, ob;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    uint32_t lo[2], hi[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int i = 2 * e + u;
+      const float xj = xa[i] * inv * wa[i];
+      const float xk = xb[i] * inv * wb[i];
+      lo[u] = narrow16<DT>(xj * ca[i] - xk * sa[i]);
+      hi[u] = narrow16<DT>(xk * cb[i] + xj * sb[i]);
+    }
+    oa[e] = lo[0] | (lo[1] << 16);
+    ob[e] = hi[0] | (hi[1] << 16);
+  }
+  uint16_t* dst = is_q ? p.q_out + ((int64_t)head * p.rows + r) * p.hd
+                       : p.k_cache + ((int64_t)head * p.cap + p.start + r) * p.hd;
+  *reinterpret_cast<u32x4*>(dst + 8 * c) = oa;
+  *reinterpret_cast<u32x4*>(dst + half + 8 * c) = ob;
+}
+
 // Column of key t in the transposed V cache: bits 2 and 3 of t swapped, so
 // each aligned group of 16 keys is stored 0-3, 8-11, 4-7, 12-15 -- the key
 // order in which the attention kernel's P.V fragments hold them.
@@ -171,16 +262,28 @@ hipError_t launch_rms_norm(int dtype, const RmsParams& p, hipStream_t s) {
   return hipGetLastError();
 }
 
+// The 16-byte form needs hd in {64, 128, 256} and every row it touches
+// 16-byte aligned (qkv rows, q / k heads, norm weights, cos / sin rows).
+bool rope_vec_ok(const RopeParams& p) {
+  auto al = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+  return (p.hd == 64 || p.hd == 128 || p.hd == 256) && p.ldqkv % 8 == 0 && al(p.qkv) &&
+         al(p.q_out) && al(p.k_cache) && al(p.qn) && al(p.kn) && al(p.cos) && al(p.sin);
+}
+
 hipError_t launch_qk_norm_rope(int dtype, const RopeParams& p, hipStream_t s) {
-  const int64_t items = p.rows * (p.nqh + p.nkvh);
   const dim3 vt((unsigned)((p.rows + 63) / 64), (unsigned)(p.hd / 64), (unsigned)p.nkvh);
+  const bool vec = rope_vec_ok(p);
+  const int slots = p.nqh + p.nkvh;
+  const int64_t items = vec ? p.rows * ((slots + 1024 / p.hd - 1) / (1024 / p.hd))
+                            : p.rows * slots;
+  const dim3 grid((unsigned)((items + 3) / 4));
   if (dtype == QA_BF16) {
-    hipLaunchKernelGGL(qk_norm_rope_kernel<QA_BF16>, dim3((unsigned)((items + 3) / 4)), dim3(256),
-                       0, s, p);
+    if (vec) hipLaunchKernelGGL(qk_norm_rope_vec_kernel<QA_BF16>, grid, dim3(256), 0, s, p);
+    else hipLaunchKernelGGL(qk_norm_rope_kernel<QA_BF16>, grid, dim3(256), 0, s, p);
     hipLaunchKernelGGL(v_transpose_kernel<QA_BF16>, vt, dim3(256), 0, s, p);
   } else {
-    hipLaunchKernelGGL(qk_norm_rope_kernel<QA_F16>, dim3((unsigned)((items + 3) / 4)), dim3(256),
-                       0, s, p);
+    if (vec) hipLaunchKernelGGL(qk_norm_rope_vec_kernel<QA_F16>, grid, dim3(256), 0, s, p);
+    else hipLaunchKernelGGL(qk_norm_rope_kernel<QA_F16>, grid, dim3(256), 0, s, p);
     hipLaunchKernelGGL(v_transpose_kernel<QA_F16>, vt, dim3(256), 0, s, p);
   }
   return hipGetLastError();

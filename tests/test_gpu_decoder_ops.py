@@ -72,10 +72,10 @@ def test_rms_norm(ctx, pkg, orc, dtype, rows, n, pad):
 
 # ------------------------------------------------- q/k norm + RoPE + KV write
 
-def _rope_case(ctx, pkg, orc, dtype, rows, nqh, nkvh, hd, pos0, start, cap, seed):
+def _rope_case(ctx, pkg, orc, dtype, rows, nqh, nkvh, hd, pos0, start, cap, seed, ld_pad=8):
     rng = np.random.default_rng(seed)
     width = (nqh + 2 * nkvh) * hd
-    ld = width + 8
+    ld = width + ld_pad
     qkv = _h16(orc, 2.0 * rng.standard_normal((rows, ld)), dtype)
     qn = (1.0 + 0.2 * rng.standard_normal(hd)).astype(np.float32)
     kn = (1.0 + 0.2 * rng.standard_normal(hd)).astype(np.float32)
@@ -115,6 +115,18 @@ def test_qk_norm_rope(ctx, pkg, orc, dtype, rows, nqh, nkvh, hd, pos0, start, ca
     _assert_1ulp(kc[:, start:start + rows], wkc[:, start:start + rows], orc, dtype)
     assert (kc[:, :start] == 0x1234).all() and (kc[:, start + rows:] == 0x1234).all()
     assert np.array_equal(vc, wvc)  # verbatim, permuted, untouched elsewhere
+
+
+@DTYPES
+def test_qk_norm_rope_unaligned_rows(ctx, pkg, orc, dtype):
+    """A row stride that is not a multiple of 8 elements takes the
+    element-wise kernel (the 16-byte one needs aligned rows); same bar."""
+    rows, nqh, nkvh, hd, start, cap = 45, 16, 8, 128, 3, 64
+    (q, kc, vc), (wq, wkc, wvc) = _rope_case(ctx, pkg, orc, dtype, rows, nqh, nkvh, hd, 2, start,
+                                             cap, 77, ld_pad=3)
+    _assert_1ulp(q, wq, orc, dtype)
+    _assert_1ulp(kc[:, start:start + rows], wkc[:, start:start + rows], orc, dtype)
+    assert np.array_equal(vc, wvc)
 
 
 # ------------------------------------------------------------- attention
