@@ -5,7 +5,7 @@
 // src/mel.rs:203-243; chunking, src/audio_encoder_gpu.rs:1079-1091).  The
 // reference runs this on the CPU with an f32 FFT; here a block transforms 16
 // frames at once as a direct DFT from LDS (400 x 201 multiply-adds per
-// frame, ~5 GFLOP for 300 s, far below the towers' cost), accumulated in f64:
+// frame, ~10 GFLOP of f64 for 300 s), accumulated in f64:
 // an f32 direct DFT would lose relative accuracy on bins 6+ decades below the
 // frame's peak, which the log-mel keeps (its floor is the clip max - 8), so
 // the transform is made effectively exact and the mel, log and clamp run in
@@ -34,8 +34,13 @@ __device__ __forceinline__ int64_t reflect(int64_t i, int64_t n) {
 }
 
 // Frames f0..f0+15: windowed samples in LDS, power spectra, mel bins, log10.
+// The windowed samples sit transposed, xw[j][f], so the DFT loop reads the 16
+// frames' sample j as four 16-byte broadcasts.  Each bin's twiddle advances by
+// a complex multiply per step (f64) and is re-anchored to the exact table
+// value every kAnchor steps, so its drift stays at a few f64 ulps.
+constexpr int kAnchor = 50;
 __global__ void __launch_bounds__(256) mel_log_kernel(const MelParams p) {
-  __shared__ float xw[FB][NFFT];
+  __shared__ __attribute__((aligned(16))) float xw[NFFT][FB];
   __shared__ float pw[FB][NBIN + 3];
   __shared__ double tc[NFFT], ts[NFFT];
   __shared__ float red[256];
@@ -57,41 +62,65 @@ __global__ void __launch_bounds__(256) mel_log_kernel(const MelParams p) {
       const int64_t src = reflect((f0 + f) * HOP + j - NFFT / 2, p.n);
       v = p.x[src] * (float)(0.5 * (1.0 - tc[j]));
     }
-    xw[f][j] = v;
+    xw[j][f] = v;
   }
   __syncthreads();
-  // one thread per bin k: the 16 frames' DFT at k, twiddle index j k mod 400
+  // one thread per bin k: the 16 frames' DFT at k
   if (tid < NBIN) {
     const int k = tid;
     double re[FB], im[FB];
 #pragma unroll
     for (int f = 0; f < FB; ++f) re[f] = im[f] = 0.0;
-    int idx = 0;
-    for (int j = 0; j < NFFT; ++j) {
-      const double c = tc[idx], s = ts[idx];
+    const double rr = tc[k], ri = -ts[k];  // e^{-2 pi i k / 400}
+    double wr = 1.0, wi = 0.0;
+    for (int j0 = 0; j0 < NFFT; j0 += kAnchor) {
+      const int idx = (j0 * k) % NFFT;
+      wr = tc[idx];
+      wi = -ts[idx];
+      for (int j = j0; j < j0 + kAnchor; ++j) {
+        typedef float f32x4 __attribute__((ext_vector_type(4)));
+        const f32x4* row = reinterpret_cast<const f32x4*>(&xw[j][0]);
 #pragma unroll
-      for (int f = 0; f < FB; ++f) {
-        re[f] += (double)xw[f][j] * c;
-        im[f] -= (double)xw[f][j] * s;
+        for (int q = 0; q < FB / 4; ++q) {
+          const f32x4 x4 = row[q];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            re[4 * q + e] += (double)x4[e] * wr;
+            im[4 * q + e] += (double)x4[e] * wi;
+          }
+        }
+        const double nr = wr * rr - wi * ri;
+        wi = wr * ri + wi * rr;
+        wr = nr;
       }
-      idx += k;
-      if (idx >= NFFT) idx -= NFFT;
     }
 #pragma unroll
     for (int f = 0; f < FB; ++f) pw[f][k] = (float)(re[f] * re[f] + im[f] * im[f]);
   }
   __syncthreads();
-  // mel m of frame f: sum_k filt[m][k] pw[f][k]; log10(max(., 1e-10))
+  // mel m of the 16 frames: sum_k filt[m][k] pw[f][k] in k order, skipping the
+  // filter's zero bins (adding 0 * pw leaves the sum unchanged), then
+  // log10(max(., 1e-10)).
   float mx = -INFINITY;
-  for (int i = tid; i < p.n_mels * FB; i += 256) {
-    const int m = i % p.n_mels, f = i / p.n_mels;
-    if (f0 + f >= p.frames) continue;
+  for (int m = tid; m < p.n_mels; m += 256) {
+    float acc[FB];
+#pragma unroll
+    for (int f = 0; f < FB; ++f) acc[f] = 0.f;
     const float* fr = p.filt + (int64_t)m * NBIN;
-    float acc = 0.f;
-    for (int k = 0; k < NBIN; ++k) acc += fr[k] * pw[f][k];
-    const float v = logf(fmaxf(acc, 1e-10f)) * (1.0f / 2.302585092994046f);
-    p.logmel[(int64_t)m * p.frames + f0 + f] = v;
-    mx = fmaxf(mx, v);
+    for (int k = 0; k < NBIN; ++k) {
+      const float w = fr[k];
+      if (w != 0.f) {
+#pragma unroll
+        for (int f = 0; f < FB; ++f) acc[f] += w * pw[f][k];
+      }
+    }
+#pragma unroll
+    for (int f = 0; f < FB; ++f) {
+      if (f0 + f >= p.frames) continue;
+      const float v = logf(fmaxf(acc[f], 1e-10f)) * (1.0f / 2.302585092994046f);
+      p.logmel[(int64_t)m * p.frames + f0 + f] = v;
+      mx = fmaxf(mx, v);
+    }
   }
   red[tid] = mx;
   __syncthreads();
