@@ -247,8 +247,11 @@ __global__ void __launch_bounds__(NS * REP * 2 * 64) attention_kernel(const Attn
   u32x4 pf[4], pl[4];
 
   // MFMA phase of step it: P.V of step it - 1 (V slot (it - 1) & 1) and
-  // S = K.Q^T of step it (K slot it & 1), interleaved so that consecutive
-  // MFMAs feed different accumulators.
+  // S = K.Q^T of step it (K slot it & 1).  Per 16-deep slice st: the P.V
+  // MFMAs of the value terms, the two S MFMAs, then the residue terms, so the
+  // two MFMAs on one O accumulator are never adjacent; the fragments of
+  // slice st + 1 are read from LDS while slice st multiplies (the schedule
+  // groups below keep the compiler from sinking the reads next to their use).
   auto mma = [&](auto pv_tag, auto s_tag, int it) {
     constexpr bool PV = decltype(pv_tag)::value, SQ = decltype(s_tag)::value;
     const unsigned char* sk = kslot(it);
@@ -257,34 +260,59 @@ __global__ void __launch_bounds__(NS * REP * 2 * 64) attention_kernel(const Attn
       s[0] = f32x16{0};
       s[1] = f32x16{0};
     }
+    auto rd_v = [&](int st, u32x4* vf) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int q = 2 * st + u, dt = q & 3, j = q >> 2;
+        const int d = dt * 32 + fr;
+        vf[u] = *reinterpret_cast<const u32x4*>(sv + d * 128 + (((2 * j + fh) ^ vswz(d)) << 4));
+      }
+    };
+    auto rd_k = [&](int st, u32x4* kf) {
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        const int r = kt * 32 + fr;
+        kf[kt] = *reinterpret_cast<const u32x4*>(sk + r * 256 + (((2 * st + fh) ^ kswz(r)) << 4));
+      }
+    };
+    u32x4 vf[2][2], kf[2][2];
+    if constexpr (PV) rd_v(0, vf[0]);
+    if constexpr (SQ) rd_k(0, kf[0]);
 #pragma unroll
     for (int st = 0; st < 8; ++st) {
-      if constexpr (SQ) {
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-          const int r = kt * 32 + fr;
-          const u32x4 kf =
-              *reinterpret_cast<const u32x4*>(sk + r * 256 + (((2 * st + fh) ^ kswz(r)) << 4));
-          s[kt] = AFmt<DT>::mfma(kf, qf[st], s[kt]);
-        }
+      const int cur = st & 1, nxt = cur ^ 1;
+      if (st + 1 < 8) {
+        if constexpr (PV) rd_v(st + 1, vf[nxt]);
+        if constexpr (SQ) rd_k(st + 1, kf[nxt]);
       }
       if constexpr (PV) {
-        u32x4 vf[2];
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
           const int q = 2 * st + u, dt = q & 3, j = q >> 2;
-          const int d = dt * 32 + fr;
-          vf[u] = *reinterpret_cast<const u32x4*>(sv + d * 128 + (((2 * j + fh) ^ vswz(d)) << 4));
-          o[dt] = AFmt<DT>::mfma(vf[u], pf[j], o[dt]);
-        }
-        if constexpr (PS == 2) {
-#pragma unroll
-          for (int u = 0; u < 2; ++u) {
-            const int q = 2 * st + u, dt = q & 3, j = q >> 2;
-            o[dt] = AFmt<DT>::mfma(vf[u], pl[j], o[dt]);
-          }
+          o[dt] = AFmt<DT>::mfma(vf[cur][u], pf[j], o[dt]);
         }
       }
+      if constexpr (SQ) {
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) s[kt] = AFmt<DT>::mfma(kf[cur][kt], qf[st], s[kt]);
+      }
+      if constexpr (PV && PS == 2) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int q = 2 * st + u, dt = q & 3, j = q >> 2;
+          o[dt] = AFmt<DT>::mfma(vf[cur][u], pl[j], o[dt]);
+        }
+      }
+    }
+    if constexpr (PV && SQ) {
+      // 4 fragment reads, then the slice's 4 or 6 MFMAs, slice by slice
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+      for (int st = 0; st < 7; ++st) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, PS == 2 ? 6 : 4, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, PS == 2 ? 6 : 4, 0);
     }
   };
 
