@@ -126,7 +126,9 @@ int Aligner::prepare(const float* x, int64_t n, int n_words, const int32_t* word
     if (word_lens[w] <= 0) return QA_EINVAL;
     for (int32_t j = 0; j < word_lens[w]; ++j) {
       const int32_t id = word_ids[off++];
-      if (id < 0 || id >= vocab) return QA_EINVAL;
+      // an audio placeholder among the words would take an audio row (the
+      // reference rejects the count mismatch, src/align_inference.rs:708-713)
+      if (id < 0 || id >= vocab || id == tok.audio_pad) return QA_EINVAL;
       ids.push_back(id);
     }
     for (int k = 0; k < 2; ++k) {
