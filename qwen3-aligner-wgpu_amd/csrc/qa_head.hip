@@ -56,44 +56,85 @@ __global__ void __launch_bounds__(256) head_norm_kernel(const HeadParams p) {
     p.normed[r * p.n + j] = ok ? widen<DT>(x[j]) * p.w[j] * inv : 0.f;
 }
 
-// logits[r][l] = sum_j normed[r][j] score[l][j] in f32: 32 rows x 64 labels per
-// block, k in slabs of 32 through LDS, 2 x 4 outputs per thread.
+// logits[r][l] = sum_j normed[r][j] score[l][j] in f32, j in order: 64 rows x
+// 64 labels per block, k in slabs of 64 through LDS stored k-major, so a
+// thread reads its 4 rows and its 4 labels of one k as two 16-byte loads and
+// does 16 FMAs with them.  The next slab is loaded into registers while the
+// current one multiplies.  VEC: rows of n floats are 16-byte aligned
+// (n % 4 == 0 and an aligned score), so each thread fetches 16 consecutive k
+// of one row / label as four 16-byte loads.
+template <bool VEC>
 __global__ void __launch_bounds__(256) head_logits_kernel(const HeadParams p) {
-  __shared__ float as[32][33], bs[64][33];
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  constexpr int KS = 64;
+  __shared__ __attribute__((aligned(16))) float as[KS][64 + 4], bs[KS][64 + 4];
   const int t = threadIdx.x;
-  const int64_t r0 = (int64_t)blockIdx.y * 32, l0 = (int64_t)blockIdx.x * 64;
-  const int tr = t >> 4, tl = t & 15;
-  float acc[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-  for (int k0 = 0; k0 < p.n; k0 += 32) {
-    for (int i = t; i < 32 * 32; i += 256) {
-      const int rr = i >> 5, kk = i & 31;
-      as[rr][kk] = (r0 + rr < p.rows && k0 + kk < p.n) ? p.normed[(r0 + rr) * p.n + k0 + kk] : 0.f;
+  const int64_t r0 = (int64_t)blockIdx.y * 64, l0 = (int64_t)blockIdx.x * 64;
+  const int tr = t >> 4, tl = t & 15;  // rows 4 tr .. 4 tr + 3, labels 4 tl .. 4 tl + 3
+  // loader: row / label ld = t / 4, k k0 + 16 (t % 4) .. + 15
+  const int ld = t >> 2, lk = (t & 3) * 16;
+  const bool arow = r0 + ld < p.rows, brow = l0 + ld < p.labels;
+  const float* ap = p.normed + (arow ? (r0 + ld) * p.n : 0);
+  const float* bp = p.score + (brow ? (l0 + ld) * p.n : 0);
+  float ra[16], rb[16];
+  auto load = [&](int k0) {
+    if constexpr (VEC) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int k = k0 + lk + 4 * q;
+        const bool in = k < p.n;  // n % 4 == 0: a chunk is all in or all out
+        const f32x4 va = (arow && in) ? *reinterpret_cast<const f32x4*>(ap + k) : f32x4{0, 0, 0, 0};
+        const f32x4 vb = (brow && in) ? *reinterpret_cast<const f32x4*>(bp + k) : f32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          ra[4 * q + e] = va[e];
+          rb[4 * q + e] = vb[e];
+        }
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int k = k0 + lk + e;
+        ra[e] = (arow && k < p.n) ? ap[k] : 0.f;
+        rb[e] = (brow && k < p.n) ? bp[k] : 0.f;
+      }
     }
-    for (int i = t; i < 64 * 32; i += 256) {
-      const int ll = i >> 5, kk = i & 31;
-      bs[ll][kk] =
-          (l0 + ll < p.labels && k0 + kk < p.n) ? p.score[(l0 + ll) * p.n + k0 + kk] : 0.f;
+  };
+  float acc[4][4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[u][i] = 0.f;
+  load(0);
+  for (int k0 = 0; k0 < p.n; k0 += KS) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      as[lk + e][ld] = ra[e];
+      bs[lk + e][ld] = rb[e];
     }
     __syncthreads();
+    if (k0 + KS < p.n) load(k0 + KS);
 #pragma unroll 8
-    for (int kk = 0; kk < 32; ++kk) {
-      const float a0 = as[2 * tr][kk], a1 = as[2 * tr + 1][kk];
+    for (int kk = 0; kk < KS; ++kk) {
+      const f32x4 a4 = *reinterpret_cast<const f32x4*>(&as[kk][4 * tr]);
+      const f32x4 b4 = *reinterpret_cast<const f32x4*>(&bs[kk][4 * tl]);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float b = bs[4 * tl + i][kk];
-        acc[0][i] += a0 * b;
-        acc[1][i] += a1 * b;
-      }
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[u][i] += a4[u] * b4[i];
     }
     __syncthreads();
   }
 #pragma unroll
-  for (int u = 0; u < 2; ++u)
+  for (int u = 0; u < 4; ++u) {
+    const int64_t r = r0 + 4 * tr + u;
+    if (r >= p.rows) continue;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int64_t r = r0 + 2 * tr + u, l = l0 + 4 * tl + i;
-      if (r < p.rows && l < p.labels) p.logits[r * p.labels + l] = acc[u][i];
+      const int64_t l = l0 + 4 * tl + i;
+      if (l < p.labels) p.logits[r * p.labels + l] = acc[u][i];
     }
+  }
 }
 
 // cls[r] = the first index of the largest logit of row r (the reference's
@@ -135,9 +176,12 @@ hipError_t launch_timestamp_head(int dtype, const HeadParams& p, hipStream_t s) 
     hipLaunchKernelGGL(head_norm_kernel<QA_BF16>, rows4, dim3(256), 0, s, p);
   else
     hipLaunchKernelGGL(head_norm_kernel<QA_F16>, rows4, dim3(256), 0, s, p);
-  hipLaunchKernelGGL(head_logits_kernel,
-                     dim3((unsigned)((p.labels + 63) / 64), (unsigned)((p.rows + 31) / 32)),
-                     dim3(256), 0, s, p);
+  const dim3 lg((unsigned)((p.labels + 63) / 64), (unsigned)((p.rows + 63) / 64));
+  if (p.n % 4 == 0 && (reinterpret_cast<uintptr_t>(p.score) & 15) == 0 &&
+      (reinterpret_cast<uintptr_t>(p.normed) & 15) == 0)
+    hipLaunchKernelGGL(head_logits_kernel<true>, lg, dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL(head_logits_kernel<false>, lg, dim3(256), 0, s, p);
   hipLaunchKernelGGL(head_argmax_kernel, rows4, dim3(256), 0, s, p);
   return hipGetLastError();
 }

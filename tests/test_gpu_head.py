@@ -106,3 +106,23 @@ def test_timestamp_head_out_of_range_position(ctx, pkg, orc):
     assert (logits[1:3] == 0).all() and cls[1] == 0 and cls[2] == 0
     _, want_c = orc.timestamp_head(F16, h, pos[[0, 3]], w, 1e-6, score)
     assert cls[0] == want_c[0] and cls[3] == want_c[1]
+
+
+def test_timestamp_head_ragged_width(ctx, pkg, orc):
+    """A hidden width that is not a multiple of 4 takes the head's scalar
+    loader (the vector one needs 16-byte rows); same bound."""
+    rng = np.random.default_rng(9)
+    n, labels, rows = 254, 70, 5
+    h = orc.h16_from_f32(rng.standard_normal((9, n)).astype(np.float32), F16)
+    w = (1.0 + 0.3 * rng.standard_normal(n)).astype(np.float32)
+    score = (0.05 * rng.standard_normal((labels, n))).astype(np.float32)
+    pos = np.array([0, 3, 8, 2, 5], np.int32)
+    logits, cls = _gpu_head(ctx, pkg, F16, h, pos, w, 1e-6, score)
+    want_l, want_c = orc.timestamp_head(F16, h, pos, w, 1e-6, score)
+    x = orc.h16_to_f32(h[pos], F16).astype(np.float64) * w
+    y = x / np.sqrt((x ** 2).mean(axis=1, keepdims=True) + 1e-6)
+    bound = (2 * n + 64) * 2.0 ** -24 * (np.abs(y) @ np.abs(score.astype(np.float64)).T)
+    assert (np.abs(logits - want_l) <= bound).all()
+    top2 = np.sort(want_l, axis=1)[:, -2:]
+    sure = top2[:, 1] - top2[:, 0] > 2 * bound.max(axis=1)
+    assert np.array_equal(cls[sure], want_c[sure])
