@@ -66,12 +66,63 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 // y[r] = r16((x - mean) * inv_std * w + b), one wave per row, 16-byte chunks;
 // mean, then the variance of (x - mean), in f32 (src/audio_encoder.rs:147-171).
-template <int DT>
+// NC > 0: rows of at most NC * 512 elements stay in registers (lane l holds
+// chunks l and l + 64, ...) and w / b come as 16-byte loads (16-byte aligned);
+// NC = 0: any width, re-reading the row.  Both sum in the same lane order.
+template <int DT, int NC>
 __global__ void __launch_bounds__(256) layer_norm_kernel(const LnParams p) {
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
   const int lane = threadIdx.x & 63;
   const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (r >= p.rows) return;
   const uint16_t* x = p.x + r * p.ldx;
+  uint16_t* y = p.y + r * p.ldy;
+  if constexpr (NC > 0) {
+    u32x4 v[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int i = lane * 8 + c * 512;
+      v[c] = i < p.n ? *reinterpret_cast<const u32x4*>(x + i) : u32x4{0, 0, 0, 0};
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+      if (lane * 8 + c * 512 < p.n) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) s += H<DT>::widen(v[c][e] & 0xffffu) + H<DT>::widen(v[c][e] >> 16);
+      }
+    const float mean = wave_sum(s) / (float)p.n;
+    float q = 0.f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+      if (lane * 8 + c * 512 < p.n) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float a = H<DT>::widen(v[c][e] & 0xffffu) - mean, b = H<DT>::widen(v[c][e] >> 16) - mean;
+          q += a * a;
+          q += b * b;
+        }
+      }
+    const float inv = 1.0f / sqrtf(wave_sum(q) / (float)p.n + p.eps);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int i = lane * 8 + c * 512;
+      if (i >= p.n) continue;
+      const f32x4 w0 = *reinterpret_cast<const f32x4*>(p.w + i), w1 = *reinterpret_cast<const f32x4*>(p.w + i + 4);
+      const f32x4 b0 = *reinterpret_cast<const f32x4*>(p.b + i), b1 = *reinterpret_cast<const f32x4*>(p.b + i + 4);
+      const float wv[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
+      const float bv[8] = {b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
+      u32x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float a = (H<DT>::widen(v[c][e] & 0xffffu) - mean) * inv * wv[2 * e] + bv[2 * e];
+        const float b = (H<DT>::widen(v[c][e] >> 16) - mean) * inv * wv[2 * e + 1] + bv[2 * e + 1];
+        o[e] = H<DT>::pack2(a, b);
+      }
+      *reinterpret_cast<u32x4*>(y + i) = o;
+    }
+    return;
+  }
   float s = 0.f;
   for (int i = lane * 8; i < p.n; i += 512) {
     const u32x4 v = *reinterpret_cast<const u32x4*>(x + i);
@@ -90,7 +141,6 @@ __global__ void __launch_bounds__(256) layer_norm_kernel(const LnParams p) {
     }
   }
   const float inv = 1.0f / sqrtf(wave_sum(q) / (float)p.n + p.eps);
-  uint16_t* y = p.y + r * p.ldy;
   for (int i = lane * 8; i < p.n; i += 512) {
     const u32x4 v = *reinterpret_cast<const u32x4*>(x + i);
     u32x4 o;
@@ -264,10 +314,15 @@ __global__ void __launch_bounds__(256) window_attention_kernel(const WinAttnPara
 
 hipError_t launch_layer_norm(int dtype, const LnParams& p, hipStream_t s) {
   const unsigned blocks = (unsigned)((p.rows + 3) / 4);
-  if (dtype == QA_BF16)
-    hipLaunchKernelGGL(layer_norm_kernel<QA_BF16>, dim3(blocks), dim3(256), 0, s, p);
-  else
-    hipLaunchKernelGGL(layer_norm_kernel<QA_F16>, dim3(blocks), dim3(256), 0, s, p);
+  const bool reg = p.n <= 1024 && (reinterpret_cast<uintptr_t>(p.w) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(p.b) & 15) == 0;
+  if (dtype == QA_BF16) {
+    if (reg) hipLaunchKernelGGL((layer_norm_kernel<QA_BF16, 2>), dim3(blocks), dim3(256), 0, s, p);
+    else hipLaunchKernelGGL((layer_norm_kernel<QA_BF16, 0>), dim3(blocks), dim3(256), 0, s, p);
+  } else {
+    if (reg) hipLaunchKernelGGL((layer_norm_kernel<QA_F16, 2>), dim3(blocks), dim3(256), 0, s, p);
+    else hipLaunchKernelGGL((layer_norm_kernel<QA_F16, 0>), dim3(blocks), dim3(256), 0, s, p);
+  }
   return hipGetLastError();
 }
 

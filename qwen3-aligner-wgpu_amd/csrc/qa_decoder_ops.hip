@@ -38,12 +38,54 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 // y[r] = r16(x[r] * inv * w), one wave per row, 8 elements per lane per step.
-template <int DT>
+// NC > 0: rows of at most NC * 512 elements stay in registers and w comes as
+// 16-byte loads (16-byte aligned); NC = 0: any width, re-reading the row.
+// Both sum in the same lane order.
+template <int DT, int NC>
 __global__ void __launch_bounds__(256) rms_norm_kernel(const RmsParams p) {
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
   const int lane = threadIdx.x & 63;
   const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (r >= p.rows) return;
   const uint16_t* x = p.x + r * p.ldx;
+  uint16_t* y = p.y + r * p.ldy;
+  if constexpr (NC > 0) {
+    u32x4 v[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int i = lane * 8 + c * 512;
+      v[c] = i < p.n ? *reinterpret_cast<const u32x4*>(x + i) : u32x4{0, 0, 0, 0};
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+      if (lane * 8 + c * 512 < p.n) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float lo = widen16<DT>(v[c][e] & 0xffffu), hi = widen16<DT>(v[c][e] >> 16);
+          s += lo * lo;
+          s += hi * hi;
+        }
+      }
+    s = wave_sum(s);
+    const float inv = 1.0f / sqrtf(s / (float)p.n + p.eps);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int i = lane * 8 + c * 512;
+      if (i >= p.n) continue;
+      const f32x4 w0 = *reinterpret_cast<const f32x4*>(p.w + i), w1 = *reinterpret_cast<const f32x4*>(p.w + i + 4);
+      const float wv[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
+      u32x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float lo = widen16<DT>(v[c][e] & 0xffffu) * inv * wv[2 * e];
+        const float hi = widen16<DT>(v[c][e] >> 16) * inv * wv[2 * e + 1];
+        o[e] = narrow16<DT>(lo) | (narrow16<DT>(hi) << 16);
+      }
+      *reinterpret_cast<u32x4*>(y + i) = o;
+    }
+    return;
+  }
   float s = 0.f;
   for (int i = lane * 8; i < p.n; i += 512) {
     const u32x4 v = *reinterpret_cast<const u32x4*>(x + i);
@@ -56,7 +98,6 @@ __global__ void __launch_bounds__(256) rms_norm_kernel(const RmsParams p) {
   }
   s = wave_sum(s);
   const float inv = 1.0f / sqrtf(s / (float)p.n + p.eps);
-  uint16_t* y = p.y + r * p.ldy;
   for (int i = lane * 8; i < p.n; i += 512) {
     const u32x4 v = *reinterpret_cast<const u32x4*>(x + i);
     u32x4 o;
@@ -255,10 +296,14 @@ __global__ void __launch_bounds__(256) v_transpose_kernel(const RopeParams p) {
 
 hipError_t launch_rms_norm(int dtype, const RmsParams& p, hipStream_t s) {
   const unsigned blocks = (unsigned)((p.rows + 3) / 4);
-  if (dtype == QA_BF16)
-    hipLaunchKernelGGL(rms_norm_kernel<QA_BF16>, dim3(blocks), dim3(256), 0, s, p);
-  else
-    hipLaunchKernelGGL(rms_norm_kernel<QA_F16>, dim3(blocks), dim3(256), 0, s, p);
+  const bool reg = p.n <= 1024 && (reinterpret_cast<uintptr_t>(p.w) & 15) == 0;
+  if (dtype == QA_BF16) {
+    if (reg) hipLaunchKernelGGL((rms_norm_kernel<QA_BF16, 2>), dim3(blocks), dim3(256), 0, s, p);
+    else hipLaunchKernelGGL((rms_norm_kernel<QA_BF16, 0>), dim3(blocks), dim3(256), 0, s, p);
+  } else {
+    if (reg) hipLaunchKernelGGL((rms_norm_kernel<QA_F16, 2>), dim3(blocks), dim3(256), 0, s, p);
+    else hipLaunchKernelGGL((rms_norm_kernel<QA_F16, 0>), dim3(blocks), dim3(256), 0, s, p);
+  }
   return hipGetLastError();
 }
 
