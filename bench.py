@@ -231,7 +231,9 @@ def bench_e2e(pkg, ctx, warmup, steps):
     log-mel -> 18-layer audio tower -> embedding gather + audio scatter ->
     28-layer decoder prefill -> timestamp head, one hipGraph per step with
     the samples and the assembled input resident in HBM.  Also times the
-    eager forward with the classes' readback and the host repair, and
+    eager forward with the classes' readback and the host repair, the same
+    forward with single-rounded probabilities (the reference GPU's softmax
+    storage, `p16_ms`), and
     compares the classes with the oracle's (the committed fixture made from
     the same seeded inputs by tests/golden/make_e2e_golden.py)."""
     from qwen3_aligner_wgpu_amd import synthetic as syn
@@ -252,6 +254,13 @@ def bench_e2e(pkg, ctx, warmup, steps):
             al.result()
         eager_ms = (time.perf_counter() - t0) * 1e3 / reps
         classes = al.read("classes")
+        # the same forward with the probabilities rounded once to 16 bits before
+        # P.V, as the reference's own GPU softmax stores them (QA_ATTN_P16)
+        dec.set_attention_flags(pkg.QA_ATTN_P16)
+        ev16, wall16 = al.time(warmup, steps, use_graph=True)
+        al.forward()
+        classes16 = al.read("classes")
+        dec.set_attention_flags(0)
     finally:
         al.close()
         enc.close()
@@ -263,6 +272,7 @@ def bench_e2e(pkg, ctx, warmup, steps):
         "eager_with_readback_ms": round(eager_ms, 3),
         "phase_ms": {k: round(v, 3) for k, v in phases.items()},
         "seq": info["seq"], "audio_tokens": info["n_audio"], "slots": info["slots"],
+        "p16_ms": round(max(ev16, wall16), 3),
     }
     try:
         gold = json.load(open(E2E_GOLDEN))
@@ -272,6 +282,7 @@ def bench_e2e(pkg, ctx, warmup, steps):
             out["argmax_identical_slots"] = int((classes == want).sum())
             out["argmax_clear_margin_slots"] = int(clear.sum())
             out["argmax_identical_at_clear_slots"] = bool((classes == want)[clear].all())
+            out["p16_argmax_identical_slots"] = int((classes16 == want).sum())
     except (OSError, KeyError, ValueError):
         out["argmax_identical_slots"] = None
     return out
