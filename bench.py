@@ -106,14 +106,39 @@ def cpu_baseline(orc, host, m, budget_s):
         t_used += time.perf_counter() - t0
         done += 1
         li += 1
+    threads = orc.num_threads()
+    # the same layer's qkv projection on one thread
+    orc.set_threads(1)
+    try:
+        w = decoder_weights(host, 0)
+        qkv_w = np.concatenate([w["q"], w["k"], w["v"]])
+        t0 = time.perf_counter()
+        orc.linear(0, normed, qkv_w, np.zeros((m, qkv_w.shape[0]), np.uint16))
+        t1 = time.perf_counter() - t0
+    finally:
+        orc.set_threads(threads)
+    cpu_model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
     return {
         "value": round(done * layer_flops / t_used / 1e12, 4),
         "unit": "TFLOP/s",
-        "cores": orc.num_threads(),
+        "cores": threads,
         "kind": "port",
         "sample": f"{done} of 28 decoder layers (4 projections each, M={m}, f16 in/out, f32 "
-                  f"accumulate) through oracle/qa_oracle.c on {orc.num_threads()} OpenMP threads; "
+                  f"accumulate) through oracle/qa_oracle.c on {threads} OpenMP threads; "
                   f"{t_used:.1f} s",
+        "value_1thread": round(per["qkv"] / t1 / 1e12, 4),
+        "sample_1thread": f"layer 0's qkv projection ({per['qkv'] / 1e9:.2f} GFLOP) on 1 thread; "
+                          f"{t1:.2f} s",
+        "cpu_model": cpu_model,
+        "nproc": os.cpu_count(),
+        "omp_num_threads": os.environ.get("OMP_NUM_THREADS"),
     }
 
 

@@ -110,6 +110,8 @@ def lib() -> ctypes.CDLL:
         L.or_timestamp_head.restype = None
         L.or_vperm.restype = i64
         L.or_num_threads.restype = ctypes.c_int
+        L.or_set_threads.argtypes = [ci]
+        L.or_set_threads.restype = None
         _lib = L
     return _lib
 
@@ -217,6 +219,10 @@ def linear(dtype: int, a: np.ndarray, w: np.ndarray, c: np.ndarray, *, flags: in
 
 def num_threads() -> int:
     return lib().or_num_threads()
+
+
+def set_threads(n: int) -> None:
+    lib().or_set_threads(n)
 
 
 def rms_norm(dtype: int, x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:

@@ -107,6 +107,15 @@ int or_num_threads(void) {
 #endif
 }
 
+/* Thread count of later parallel regions (the CPU baseline's 1-thread figure). */
+void or_set_threads(int n) {
+#ifdef _OPENMP
+  if (n > 0) omp_set_num_threads(n);
+#else
+  (void)n;
+#endif
+}
+
 /* ------------------------------------------------------------------------ */
 /* f32 GEMM: restates gemm_row_major (src/cpu_decoder.rs:583-610,
  * src/cpu_tensor.rs:82-108): dst = beta*dst + x.W^T, row-major x [m,k] and

@@ -94,6 +94,7 @@ int or_linear(const or_linear_desc* d);
 
 /* Number of OpenMP threads the oracle's parallel loops use. */
 int or_num_threads(void);
+void or_set_threads(int n);
 
 /* ---- decoder prefill ops around the projections (qa_oracle_decoder.c) ----
  * Parity pins (tests/test_oracle_decoder.py): f64 closed forms of RMSNorm and

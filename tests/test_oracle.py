@@ -312,3 +312,27 @@ def test_linear_rejects_bad_descriptors(orc):
         orc.linear(orc.F16, a, w, c, flags=orc.EPI_SILU_MUL, bias=np.zeros(8, np.uint16))
     with pytest.raises(ValueError):
         orc.linear(7, a, w, c)
+
+
+def test_linear_fixtures_regression(orc, pkg):
+    """The oracle's linear outputs (f64-exact and f32 modes, every epilogue,
+    f16 and bf16, M in {1, 7, 64}, K in {16, 1024}) on seeded inputs match the
+    digests committed in tests/golden/linear_fixtures.json (written by
+    tests/golden/make_linear_fixtures.py): a change to the oracle's arithmetic
+    or rounding points shows here."""
+    import importlib.util
+    import json
+    import os
+    here = os.path.dirname(os.path.abspath(__file__))
+    spec = importlib.util.spec_from_file_location(
+        "make_linear_fixtures", os.path.join(here, "golden", "make_linear_fixtures.py"))
+    mk = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mk)
+    from qwen3_aligner_wgpu_amd import host
+    fx = json.load(open(os.path.join(here, "golden", "linear_fixtures.json")))["cases"]
+    assert len(fx) == len(list(mk.cases()))
+    for c in fx:
+        case = {k: c[k] for k in ("dtype", "m", "n", "k", "epi")}
+        exact, f32 = mk.run(orc, host, case)
+        assert mk.digest(exact) == c["exact"], case
+        assert mk.digest(f32) == c["f32"], case
