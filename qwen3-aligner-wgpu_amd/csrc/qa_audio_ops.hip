@@ -189,7 +189,6 @@ __global__ void __launch_bounds__(256) add_table_kernel(const TableAddParams p) 
 // group of 16 keys, 0-3, 8-11, 4-7, 12-15 (bits 2 and 3 swapped).
 constexpr int WA_HD = 64, WA_MAXW = 128;
 
-__device__ __forceinline__ int wa_vperm(int t) { return (t & ~12) | ((t & 4) << 1) | ((t & 8) >> 1); }
 
 template <int DT>
 __global__ void __launch_bounds__(256) window_attention_kernel(const WinAttnParams p) {
@@ -204,23 +203,40 @@ __global__ void __launch_bounds__(256) window_attention_kernel(const WinAttnPara
   const int64_t dm = (int64_t)p.nh * WA_HD;
   const uint16_t* qkv = p.qkv + st * p.ldqkv + (int64_t)h * WA_HD;
 
-  // ---- K rows (chunk c of row r at c ^ ((r >> 1) & 7)) and V^T into LDS ----
+  // ---- K rows (chunk c of row r at c ^ ((r >> 1) & 7)) into LDS ----
   for (int i = tid; i < WA_MAXW * 8; i += 256) {
     const int r = i >> 3, c = i & 7;
-    u32x4 kv = {0, 0, 0, 0}, vv = {0, 0, 0, 0};
-    if (r < len) {
-      kv = *reinterpret_cast<const u32x4*>(qkv + (int64_t)r * p.ldqkv + dm + c * 8);
-      vv = *reinterpret_cast<const u32x4*>(qkv + (int64_t)r * p.ldqkv + 2 * dm + c * 8);
-    }
+    u32x4 kv = {0, 0, 0, 0};
+    if (r < len) kv = *reinterpret_cast<const u32x4*>(qkv + (int64_t)r * p.ldqkv + dm + c * 8);
     *reinterpret_cast<u32x4*>(ks + r * WA_HD + ((c ^ ((r >> 1) & 7)) << 3)) = kv;
-    // V^T row d: 16 chunks of 8 stored keys, chunk k at k ^ (d & 15)
-    const int col = wa_vperm(r);
+  }
+  // ---- V^T into LDS, 8 x 8 blocks transposed in registers ----
+  // Thread t < 128 takes stored-key chunk sc = t / 8 (8 stored columns) and
+  // d chunk c = t % 8: stored columns 16 g + 8 h + 0..7 hold keys
+  // 16 g + 4 h + 0..3 and 16 g + 8 + 4 h + 0..3 (bits 2 and 3 of the key
+  // swapped), so it loads those
+  // 8 key rows of V (16 bytes each) and writes 8 V^T rows d = 8 c .. 8 c + 7,
+  // 16 bytes each, at chunk sc ^ (d & 15) (row d: 16 chunks of 8 stored keys).
+  if (tid < 128) {
+    const int sc = tid >> 3, c = tid & 7;
+    const int g = sc >> 1, hh = sc & 1;
+    u32x4 vr[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int key = 16 * g + 8 * (j >> 2) + 4 * hh + (j & 3);  // stored column 8 sc + j
+      vr[j] = key < len ? *reinterpret_cast<const u32x4*>(qkv + (int64_t)key * p.ldqkv + 2 * dm + c * 8)
+                        : u32x4{0, 0, 0, 0};
+    }
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const int d = c * 8 + e;
-      const uint32_t word = vv[e >> 1];
-      vts[d * WA_MAXW + ((((col >> 3) ^ (d & 15)) << 3) | (col & 7))] =
-          (uint16_t)((e & 1) ? word >> 16 : word & 0xffffu);
+      u32x4 o;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t a = vr[2 * q][e >> 1], b = vr[2 * q + 1][e >> 1];
+        o[q] = (e & 1) ? ((a >> 16) | (b & 0xffff0000u)) : ((a & 0xffffu) | (b << 16));
+      }
+      *reinterpret_cast<u32x4*>(vts + d * WA_MAXW + ((sc ^ (d & 15)) << 3)) = o;
     }
   }
   // ---- this wave's query rows as B fragments (4 slices of 16 d) ----
