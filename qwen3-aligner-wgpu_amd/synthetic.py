@@ -46,13 +46,14 @@ def synthetic_words(n: int, seed: int) -> list[str]:
 
 def word_token_ids(word: str, vocab: int = TEXT_VOCAB) -> list[int]:
     """Stand-in for the checkpoint's BPE tokenizer (absent here): the word in
-    pieces of up to 5 letters, each piece an id in [0, vocab) from its FNV-1a
-    hash, so a 2-8 letter word costs 1-2 ids (the reference's 15 s clip
-    spends 48 BPE ids on 39 words).  The ids stay below the special tokens."""
+    pieces of up to 4 letters (ceil(len / 4) ids), each piece an id in
+    [0, vocab) from its FNV-1a hash, so a 2-8 letter word costs 1-2 ids (the
+    reference's 15 s clip spends 48 BPE ids on 39 words).  The ids stay below
+    the special tokens."""
     ids = []
-    for i in range(0, len(word), 5):
+    for i in range(0, len(word), 4):
         h = 0xcbf29ce484222325
-        for ch in word[i:i + 5].encode():
+        for ch in word[i:i + 4].encode():
             h = ((h ^ ch) * 0x100000001b3) & 0xFFFFFFFFFFFFFFFF
         ids.append(int(h % vocab))
     return ids
@@ -61,8 +62,8 @@ def word_token_ids(word: str, vocab: int = TEXT_VOCAB) -> list[int]:
 def aligner_weights(dtype: int, enc_layers: int, dec_layers: int, seed: int = 5) -> dict:
     """Random-init weights: linears ~ N(0, 0.02) with biases ~ N(0, 0.01)
     (the tower's), conv weights ~ N(0, 1/fan_in) with biases ~ N(0, 0.05),
-    norm weights ~ 1 + N(0, 0.1) with LayerNorm biases ~ N(0, 0.1), the token
-    embedding ~ N(0, 1), the score head ~ N(0, 0.02) in f32.
+    every norm weight 1 and every LayerNorm bias 0, the token embedding
+    ~ N(0, 0.02), the score head ~ N(0, 0.02) in f32.
 
     Returns {"enc": {conv, co, layers, post}, "dec": [layer dicts],
     "embed", "norm_w", "score"} in the checkpoint's layouts ([out][in]
@@ -79,13 +80,13 @@ def aligner_weights(dtype: int, enc_layers: int, dec_layers: int, seed: int = 5)
     for li in range(enc_layers):
         b = 1000 + 16 * li
         enc["layers"].append(dict(
-            ln1=(f(b, (dm,), 1.0, 0.1), f(b + 1, (dm,), 0.0, 0.1)),
+            ln1=(f(b, (dm,), 1.0, 0.0), f(b + 1, (dm,), 0.0, 0.0)),
             qkv=(g(b + 2, (3 * dm, dm), 0.02), g(b + 3, (3 * dm,), 0.01)),
             o=(g(b + 4, (dm, dm), 0.02), g(b + 5, (dm,), 0.01)),
-            ln2=(f(b + 6, (dm,), 1.0, 0.1), f(b + 7, (dm,), 0.0, 0.1)),
+            ln2=(f(b + 6, (dm,), 1.0, 0.0), f(b + 7, (dm,), 0.0, 0.0)),
             fc1=(g(b + 8, (ff, dm), 0.02), g(b + 9, (ff,), 0.01)),
             fc2=(g(b + 10, (dm, ff), 0.02), g(b + 11, (dm,), 0.01))))
-    enc["post"] = ((f(20, (dm,), 1.0, 0.1), f(21, (dm,), 0.0, 0.1)),
+    enc["post"] = ((f(20, (dm,), 1.0, 0.0), f(21, (dm,), 0.0, 0.0)),
                    (g(22, (dm, dm), 0.02), g(23, (dm,), 0.01)),
                    (g(24, (od, dm), 0.02), g(25, (od,), 0.01)))
     hs, hd, nq, nk, it = TEXT["hidden"], TEXT["hd"], TEXT["nqh"], TEXT["nkvh"], TEXT["inter"]
@@ -97,10 +98,10 @@ def aligner_weights(dtype: int, enc_layers: int, dec_layers: int, seed: int = 5)
             v=g(b + 2, (nk * hd, hs), 0.02), o=g(b + 3, (hs, nq * hd), 0.02),
             gate=g(b + 4, (it, hs), 0.02), up=g(b + 5, (it, hs), 0.02),
             down=g(b + 6, (hs, it), 0.02),
-            iln=f(b + 7, (hs,), 1.0, 0.1), pln=f(b + 8, (hs,), 1.0, 0.1),
-            qn=f(b + 9, (hd,), 1.0, 0.1), kn=f(b + 10, (hd,), 1.0, 0.1)))
-    return dict(enc=enc, dec=dec, embed=g(30, (VOCAB, hs), 1.0),
-                norm_w=f(31, (hs,), 1.0, 0.1), score=f(32, (LABELS, hs), 0.0, 0.02))
+            iln=f(b + 7, (hs,), 1.0, 0.0), pln=f(b + 8, (hs,), 1.0, 0.0),
+            qn=f(b + 9, (hd,), 1.0, 0.0), kn=f(b + 10, (hd,), 1.0, 0.0)))
+    return dict(enc=enc, dec=dec, embed=g(30, (VOCAB, hs), 0.02),
+                norm_w=f(31, (hs,), 1.0, 0.0), score=f(32, (LABELS, hs), 0.0, 0.02))
 
 
 def build_aligner(pkg, ctx, dtype: int, w: dict, max_seconds: float, max_rows: int):
