@@ -151,7 +151,7 @@ constexpr double kReduceGBs = 3000.0;   // split-K reduce kernel, partials from 
 // Tile / split-K choice: the modelled time of each candidate is
 // rounds x (fixed + stages x stage_us) (+ the reduce kernel when K is split),
 // where rounds = ceil(units / CUs); the cheapest candidate wins.
-void choose_group_m(qa::Plan& pl);
+void choose_group_m(qa::Plan& pl, int64_t span = 0);
 
 qa::Plan plan_linear(const qa_linear_desc& d, int num_cus) {
   qa::Plan pl{};
@@ -209,12 +209,15 @@ qa::Plan plan_linear(const qa_linear_desc& d, int num_cus) {
 // about per = tiles/8 tiles, which with bands of g m-tiles covers g m-tiles
 // x ceil(per/g) n-tiles; its L2 fetches those A rows (bm each) and W rows
 // (bn each, both halves of a SiLU tile).  The cheapest g wins, the whole
-// n-column order (g = tiles_m) on ties.  QA_GROUP_M forces g.
-void choose_group_m(qa::Plan& pl) {
+// n-column order (g = tiles_m) on ties.  With span > 0 the count is taken
+// over the first `span` tiles of the range instead of all of it (see
+// plan_conv).  QA_GROUP_M forces g.
+void choose_group_m(qa::Plan& pl, int64_t span) {
   {
     const qa::TileShape ts = qa::tile_shape(pl.tile);
     const int64_t tm = pl.tiles_m, tn = pl.tiles_n;
-    const int64_t per = std::max<int64_t>(1, (tm * tn + 7) / 8);
+    int64_t per = std::max<int64_t>(1, (tm * tn + 7) / 8);
+    if (span > 0) per = std::min(per, span);
     pl.group_m = (int)tm;
     double best = 1e300;
     for (int64_t g = tm; g >= 1; g = g > 1 ? (g + 1) / 2 : 0) {
@@ -236,6 +239,16 @@ void choose_group_m(qa::Plan& pl) {
 
 // The implicit-GEMM convolution: M = output pixels, N = c_out, K = 9 c_in,
 // never split (K is long), on the tile shapes the CV loader is built for.
+// The A operand is an input slab that nine taps re-read; at the stem's sizes
+// (a 921 MB input for the second level over 300 chunks) an XCD's range of
+// tiles touches far more of it than its 4 MB L2 holds, so only the tiles
+// its CUs run at the same time (one per CU) can share what the L2 fetched:
+// the band height is chosen for that window.  For the same reason the
+// 128 x 256 tile comes first among equal costs: it gathers each input slab
+// for half as many n-tiles as 256 x 128.  Measured on the 300-chunk second
+// level (c = 480): 256 x 128 took 2.07 ms with the whole-range band (118
+// m-tiles, each slab re-fetched once per n-tile) and 1.50 ms with bands of
+// 8; 128 x 256 with the window's band takes 1.37-1.41 ms.
 qa::Plan plan_conv(int64_t M, int64_t N, int64_t K, bool gelu, int num_cus) {
   qa::Plan pl{};
   pl.epi = gelu ? qa::EPI_GELU : qa::EPI_PLAIN;
@@ -245,7 +258,7 @@ qa::Plan plan_conv(int64_t M, int64_t N, int64_t K, bool gelu, int num_cus) {
   double best = 1e300;
   int forced_tile = -1;
   if (const char* e = getenv("QA_TILE")) forced_tile = atoi(e);
-  for (const int tile : {qa::TILE_128x128, qa::TILE_256x128}) {
+  for (const int tile : {qa::TILE_128x256, qa::TILE_256x128, qa::TILE_128x128}) {
     if (forced_tile >= 0 && forced_tile != tile) continue;
     const qa::TileShape ts = qa::tile_shape(tile);
     const int64_t tm = (M + ts.bm - 1) / ts.bm, tn = (N + ts.bn - 1) / ts.bn;
@@ -263,7 +276,7 @@ qa::Plan plan_conv(int64_t M, int64_t N, int64_t K, bool gelu, int num_cus) {
     pl.tiles_m = (int)((M + 127) / 128);
     pl.tiles_n = (int)((N + 127) / 128);
   }
-  choose_group_m(pl);
+  choose_group_m(pl, std::max(1, num_cus / 8));
   return pl;
 }
 

@@ -4,8 +4,12 @@
 // src/audio_encoder.rs:376-447, c_in = 1; the GPU tower's im2col + gemm_conv +
 // bias_gelu, src/audio_encoder_gpu.rs:1165-1201,1714-1794).  With one input
 // channel the im2col row of an output pixel is 9 scattered values, which the
-// implicit GEMM's 16-byte channel chunks cannot fetch; at 9 multiply-adds per
-// output this level is bound by its output writes, not by arithmetic.
+// implicit GEMM's 16-byte channel chunks cannot fetch.  Per output it costs 9
+// multiply-adds and the erf GELU (a reciprocal, an exponential and ~15 more
+// VALU operations), ~30 VALU slots in all: over the 300-chunk stem (461 M
+// outputs) that is ~0.35 ms of the 256 CUs' VALU issue, which is what the
+// measured ~0.43 ms follows (2.1 TB/s of output writes, well under HBM's
+// rate; a variant with fully contiguous stores measured the same).
 //
 // A block takes 64 output pixels x every output channel: the 9 taps of its
 // thread's pixel stay in registers, the weights and bias sit in LDS as f32,

@@ -780,6 +780,8 @@ hipError_t launch_epi(const Plan& plan, const GemmParams& p, int batch, hipStrea
     if constexpr (EPI == EPI_SILU) return hipErrorInvalidValue;  // never planned
     else if (plan.tile == TILE_256x128)
       e = launch_dma<DT, 256, 128, 3, EPI, 2, 0, 1>(plan, p, batch, s);
+    else if (plan.tile == TILE_128x256)
+      e = launch_dma<DT, 128, 256, 3, EPI, 2, 0, 1>(plan, p, batch, s);
     else
       e = launch_dma<DT, 128, 128, 5, EPI, 2, 8, 1>(plan, p, batch, s);
   } else if (plan.transb) {

@@ -82,9 +82,9 @@ def test_conv(ctx, pkg, orc, dtype, b, h, w, c_in, c_out, tmajor):
     assert_parity(got, want, orc, dtype, ulp_tol=1)
 
 
-@pytest.mark.parametrize("tile", ["0", "1"], ids=["128x128", "256x128"])
+@pytest.mark.parametrize("tile", ["0", "1", "2"], ids=["128x128", "256x128", "128x256"])
 def test_conv_tiles_and_no_activation(ctx, pkg, orc, monkeypatch, tile):
-    """Both implicit-GEMM tile shapes, without bias and GELU (the plain sum)."""
+    """Every implicit-GEMM tile shape, without bias and GELU (the plain sum)."""
     monkeypatch.setenv("QA_TILE", tile)
     x, wt, _ = _case(orc, F16, 2, 20, 18, 96, 200, 7)
     got = _conv_gpu(ctx, pkg, F16, x, wt, None, 200, 0)
