@@ -141,6 +141,7 @@ double stage_us(int tile) {
     case qa::TILE_128x192: return 0.72;
     case qa::TILE_64x128: return 0.36;
     case qa::TILE_64x64: return 0.27;
+    case qa::TILE_256x256: return 1.75;
     default: return 0.56;
   }
 }
@@ -166,7 +167,8 @@ qa::Plan plan_linear(const qa_linear_desc& d, int num_cus) {
   if (const char* e = getenv("QA_SPLITS")) forced_splits = atoi(e);
 
   int cands[qa::TILE_COUNT] = {qa::TILE_128x128, qa::TILE_256x128, qa::TILE_128x256,
-                               qa::TILE_64x128,  qa::TILE_64x64,   qa::TILE_128x192};
+                               qa::TILE_64x128,  qa::TILE_64x64,   qa::TILE_128x192,
+                               qa::TILE_256x256};
   int ncand = qa::TILE_COUNT;
   if (pl.transb) ncand = 1;  // the conv operand path has one tile shape
   if (forced_tile >= 0 && forced_tile < qa::TILE_COUNT && !pl.transb) {
@@ -258,7 +260,7 @@ qa::Plan plan_conv(int64_t M, int64_t N, int64_t K, bool gelu, int num_cus) {
   double best = 1e300;
   int forced_tile = -1;
   if (const char* e = getenv("QA_TILE")) forced_tile = atoi(e);
-  for (const int tile : {qa::TILE_128x256, qa::TILE_256x128, qa::TILE_128x128}) {
+  for (const int tile : {qa::TILE_128x256, qa::TILE_256x128, qa::TILE_128x128, qa::TILE_256x256}) {
     if (forced_tile >= 0 && forced_tile != tile) continue;
     const qa::TileShape ts = qa::tile_shape(tile);
     const int64_t tm = (M + ts.bm - 1) / ts.bm, tn = (N + ts.bn - 1) / ts.bn;

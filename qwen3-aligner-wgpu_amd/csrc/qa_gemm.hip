@@ -319,11 +319,21 @@ __device__ __forceinline__ void finish_tile(const GemmParams& p, f32x16 (&acc)[F
   }
 }
 
-// KG k-groups of 4 MMA waves; group g multiplies slices
-// {g*4/KG .. (g+1)*4/KG - 1} of each 64-deep stage on a 2x2 wave layout, so
-// the LDS read traffic per stage does not grow with KG.  The groups' partial
-// accumulators are summed through LDS at the end, group 0 + group 1 + ..., a
-// fixed order.
+// KG k-groups of 2 x WGN MMA waves; group g multiplies slices
+// {g*4/KG .. (g+1)*4/KG - 1} of each 64-deep stage on a 2 (m) x WGN (n)
+// wave layout, so the LDS read traffic per stage does not grow with KG.  The
+// groups' partial accumulators are summed through LDS at the end, group 0 +
+// group 1 + ..., a fixed order.
+//
+// The 256 x 256 tile (one group of 2 x 4 waves of 128 x 64, two 64 KB
+// stages) halves the L2 -> LDS bytes per FLOP of the 128-wide tiles; its f32
+// staging tile (266 KB) exceeds the LDS, so it leaves in two row passes.  On
+// the prefill shapes (M ~ 4300) it wins where it also cuts the tile rounds:
+// gate|up 72 us against 94-102 us with 128 x 192 (408 tiles = 2 rounds
+// against 1088 = 5), and the stem's second conv level (1.25 ms against
+// 1.5 ms).  Four 128 x 128 waves (one per SIMD, accumulators in AGPRs) read
+// a third less LDS but measured 13-25% slower: four waves cannot issue the
+// DMA fast enough.
 //
 // Who streams L2 -> LDS: a wave sustains only ~12 GB/s of DMA however deep
 // its queue, so the CU's fill rate grows with the number of waves issuing it
@@ -340,25 +350,31 @@ __device__ __forceinline__ void finish_tile(const GemmParams& p, f32x16 (&acc)[F
 // is computed per chunk, and taps in the zero padding read as zeros through
 // the buffer resource's range check (the im2col of src/audio_encoder.rs:
 // 204-236, never materialised).
-template <int DT, int BM, int BN, int S, int EPI, int KG, int PW, int CV = 0>
-__global__ void __launch_bounds__(NT * KG + 64 * PW) gemm_dma_kernel(const GemmParams p) {
-  constexpr int NMW = 4 * KG;                // MMA waves
-  constexpr int NTH = NT * KG + 64 * PW;     // threads
+template <int DT, int BM, int BN, int S, int EPI, int KG, int PW, int CV = 0, int WGN = 2>
+__global__ void __launch_bounds__(64 * (2 * WGN * KG + PW)) gemm_dma_kernel(const GemmParams p) {
+  constexpr int WGM = 2;                     // waves along m within a group (WGN along n)
+  constexpr int GW = WGM * WGN;              // MMA waves per k group
+  constexpr int NMW = GW * KG;               // MMA waves
+  constexpr int NTH = 64 * (NMW + PW);       // threads
   constexpr int NW = PW > 0 ? PW : NMW;      // DMA-issuing waves
-  constexpr int SPG = 4 / KG;      // 16-deep slices per group per stage
-  constexpr int WGM = 2, WGN = 2;  // waves along m and n within a group
+  constexpr int SPG = 4 / KG;                // 16-deep slices per group per stage
   constexpr int WTM = BM / WGM, WTN = BN / WGN;
   constexpr int FM = WTM / 32, FN = WTN / 32;
   constexpr int AJ = BM / (8 * NW), BJ = BN / (8 * NW);  // DMA instructions per wave per stage
   constexpr int LPS = AJ + BJ;
   constexpr int SA = BM * 128, STAGE = (BM + BN) * 128;
-  constexpr int SMEM = S * STAGE;
+  // Epilogue staging: the f32 tile (rows padded by 4 floats) in EP row passes.
+  constexpr int LDT = BN + 4;
+  constexpr int EP = BM * LDT * 4 <= S * STAGE ? 1 : 2;
+  constexpr int SMEM = S * STAGE > BM / EP * LDT * 4 ? S * STAGE : BM / EP * LDT * 4;
   static_assert(KG == 1 || KG == 2 || KG == 4, "k groups");
   static_assert(FM >= 1 && FN >= 1 && AJ >= 1 && BJ >= 1, "tile shape");
   static_assert(BM % (8 * NW) == 0 && BN % (8 * NW) == 0, "DMA row groups");
   static_assert(EPI != EPI_SILU || BN % 64 == 0, "SiLU tiles hold whole gate / up subtiles");
   static_assert(S >= 2 && (S - 1) * LPS < 64, "pipeline depth");
   static_assert(KG == 1 || (KG - 1) * 4 * BM * BN <= SMEM, "reduction buffer");
+  static_assert(EP == 1 || (EP == WGM && KG == 1), "row passes follow the waves' m halves");
+  static_assert(SMEM <= 160 * 1024, "LDS");
   __shared__ __attribute__((aligned(1024))) unsigned char smem[SMEM];
 
   const int tid = threadIdx.x;
@@ -367,7 +383,7 @@ __global__ void __launch_bounds__(NT * KG + 64 * PW) gemm_dma_kernel(const GemmP
   const bool mma_wave = PW == 0 || wave < NMW;
   const bool dma_wave = PW == 0 || wave >= NMW;
   const int dwave = PW == 0 ? wave : (wave >= NMW ? wave - NMW : 0);  // index among DMA waves
-  const int kg = mma_wave ? wave >> 2 : KG, w4 = wave & 3;  // producers: no k group
+  const int kg = mma_wave ? wave / GW : KG, w4 = wave % GW;  // producers: no k group
   const int wm = w4 % WGM, wn = w4 / WGM;
   const int fr = lane & 31, fh = lane >> 5;  // fragment row, k-chunk parity
 
@@ -555,50 +571,56 @@ __global__ void __launch_bounds__(NT * KG + 64 * PW) gemm_dma_kernel(const GemmP
   // threads take consecutive 4-column groups, so bias / residual reads and
   // the 16-bit stores are contiguous row segments.  Rows are padded by 4
   // floats, which puts the 16 rows a quarter-wave writes on distinct banks.
-  constexpr int LDT = BN + 4;
-  static_assert(BM * LDT * 4 <= SMEM, "epilogue staging tile");
+  // With EP = 2 (a tile larger than the LDS) the rows leave in two passes,
+  // the m half of the waves with wm = 0, then that of wm = 1.
+  constexpr int PR = BM / EP;  // tile rows per pass
   float* tile = reinterpret_cast<float*>(smem);
-  __syncthreads();  // all stages consumed (every DMA was waited for)
-#pragma unroll
-  for (int g = 0; g < KG; ++g) {
-    if (kg == g) {
-#pragma unroll
-      for (int fm = 0; fm < FM; ++fm)
-#pragma unroll
-        for (int fn = 0; fn < FN; ++fn)
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const int row = wm * WTM + fm * 32 + fr;
-            const int col = (wn * FN + fn) * 32 + 8 * q + 4 * fh;
-            f32x4* dst = reinterpret_cast<f32x4*>(tile + row * LDT + col);
-            const f32x4 v = {acc[fm][fn][4 * q], acc[fm][fn][4 * q + 1], acc[fm][fn][4 * q + 2],
-                             acc[fm][fn][4 * q + 3]};
-            *dst = (g == 0) ? v : *dst + v;
-          }
-    }
-    __syncthreads();
-  }
   constexpr int OUTC = EPI == EPI_SILU ? BN / 2 : BN;  // output columns of the tile
   constexpr int GPR = OUTC / 4;                          // 4-column groups per row
   const int nfull = EPI == EPI_SILU ? p.N / 2 : p.N;
   const int n0 = tn * OUTC;
-  for (int idx = tid; idx < BM * GPR; idx += NTH) {
-    const int r = idx / GPR, c4 = (idx % GPR) * 4;
-    const int m = m0 + r, n = n0 + c4;
-    if (m >= p.M || n >= nfull) continue;
-    const f32x4 v4 = *reinterpret_cast<const f32x4*>(tile + r * LDT + c4);
-    f32x4 u4 = {0.f, 0.f, 0.f, 0.f};
-    if constexpr (EPI == EPI_SILU) u4 = *reinterpret_cast<const f32x4*>(tile + r * LDT + BN / 2 + c4);
-    if (p.splits > 1) {
-      f32x4* ws = reinterpret_cast<f32x4*>(p.ws);
-      const int64_t rowbase = ((int64_t)split * p.M + m) * p.N;
-      ws[(rowbase + n) >> 2] = v4;
-      if constexpr (EPI == EPI_SILU) ws[(rowbase + nfull + n) >> 2] = u4;
-      continue;
+  __syncthreads();  // all stages consumed (every DMA was waited for)
+#pragma unroll
+  for (int e = 0; e < EP; ++e) {
+    if (e > 0) __syncthreads();  // the previous pass's rows have been read
+#pragma unroll
+    for (int g = 0; g < KG; ++g) {
+      if (kg == g && (EP == 1 || wm == e)) {
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+          for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const int row = wm * WTM + fm * 32 + fr - e * PR;
+              const int col = (wn * FN + fn) * 32 + 8 * q + 4 * fh;
+              f32x4* dst = reinterpret_cast<f32x4*>(tile + row * LDT + col);
+              const f32x4 v = {acc[fm][fn][4 * q], acc[fm][fn][4 * q + 1], acc[fm][fn][4 * q + 2],
+                               acc[fm][fn][4 * q + 3]};
+              *dst = (g == 0) ? v : *dst + v;
+            }
+      }
+      __syncthreads();
     }
-    const float v[4] = {v4.x, v4.y, v4.z, v4.w};
-    const float uu[4] = {u4.x, u4.y, u4.z, u4.w};
-    epilogue4<DT, EPI>(p, C, m, n, v, uu);
+    for (int idx = tid; idx < PR * GPR; idx += NTH) {
+      const int r = idx / GPR, c4 = (idx % GPR) * 4;
+      const int m = m0 + e * PR + r, n = n0 + c4;
+      if (m >= p.M || n >= nfull) continue;
+      const f32x4 v4 = *reinterpret_cast<const f32x4*>(tile + r * LDT + c4);
+      f32x4 u4 = {0.f, 0.f, 0.f, 0.f};
+      if constexpr (EPI == EPI_SILU)
+        u4 = *reinterpret_cast<const f32x4*>(tile + r * LDT + BN / 2 + c4);
+      if (p.splits > 1) {
+        f32x4* ws = reinterpret_cast<f32x4*>(p.ws);
+        const int64_t rowbase = ((int64_t)split * p.M + m) * p.N;
+        ws[(rowbase + n) >> 2] = v4;
+        if constexpr (EPI == EPI_SILU) ws[(rowbase + nfull + n) >> 2] = u4;
+        continue;
+      }
+      const float v[4] = {v4.x, v4.y, v4.z, v4.w};
+      const float uu[4] = {u4.x, u4.y, u4.z, u4.w};
+      epilogue4<DT, EPI>(p, C, m, n, v, uu);
+    }
   }
 }
 
@@ -749,11 +771,11 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(const GemmParams p) 
   epilogue4<DT, EPI>(p, p.c, m, n, v, uu);
 }
 
-template <int DT, int BM, int BN, int S, int EPI, int KG, int PW, int CV = 0>
+template <int DT, int BM, int BN, int S, int EPI, int KG, int PW, int CV = 0, int WGN = 2>
 hipError_t launch_dma(const Plan& plan, const GemmParams& p, int batch, hipStream_t s) {
   const unsigned units = (unsigned)(plan.tiles_m * plan.tiles_n * plan.splits);
-  hipLaunchKernelGGL((gemm_dma_kernel<DT, BM, BN, S, EPI, KG, PW, CV>),
-                     dim3(units, (unsigned)batch), dim3(NT * KG + 64 * PW), 0, s, p);
+  hipLaunchKernelGGL((gemm_dma_kernel<DT, BM, BN, S, EPI, KG, PW, CV, WGN>),
+                     dim3(units, (unsigned)batch), dim3(64 * (2 * WGN * KG + PW)), 0, s, p);
   return hipGetLastError();
 }
 
@@ -782,6 +804,8 @@ hipError_t launch_epi(const Plan& plan, const GemmParams& p, int batch, hipStrea
       e = launch_dma<DT, 256, 128, 3, EPI, 2, 0, 1>(plan, p, batch, s);
     else if (plan.tile == TILE_128x256)
       e = launch_dma<DT, 128, 256, 3, EPI, 2, 0, 1>(plan, p, batch, s);
+    else if (plan.tile == TILE_256x256)
+      e = launch_dma<DT, 256, 256, 2, EPI, 1, 0, 1, 4>(plan, p, batch, s);
     else
       e = launch_dma<DT, 128, 128, 5, EPI, 2, 8, 1>(plan, p, batch, s);
   } else if (plan.transb) {
@@ -794,6 +818,7 @@ hipError_t launch_epi(const Plan& plan, const GemmParams& p, int batch, hipStrea
       case TILE_64x128: e = launch_dma<DT, 64, 128, 4, EPI, 2, 8>(plan, p, batch, s); break;
       case TILE_64x64: e = launch_dma<DT, 64, 64, 6, EPI, 2, 8>(plan, p, batch, s); break;
       case TILE_128x192: e = launch_dma<DT, 128, 192, 4, EPI, 2, 0>(plan, p, batch, s); break;
+      case TILE_256x256: e = launch_dma<DT, 256, 256, 2, EPI, 1, 0, 0, 4>(plan, p, batch, s); break;
       default: e = launch_dma<DT, 128, 128, 5, EPI, 2, 8>(plan, p, batch, s); break;
     }
   }

@@ -23,6 +23,7 @@ enum TileCfg : int {
   TILE_64x128 = 3,   // waves of 32(m) x 64(n)
   TILE_64x64 = 4,    // waves of 32x32
   TILE_128x192 = 5,  // waves of 64(m) x 96(n)
+  TILE_256x256 = 6,  // one k group of 2x4 waves of 128(m) x 64(n)
   TILE_COUNT
 };
 
@@ -36,6 +37,7 @@ inline TileShape tile_shape(int cfg) {
     case TILE_64x128: return {64, 128};
     case TILE_64x64: return {64, 64};
     case TILE_128x192: return {128, 192};
+    case TILE_256x256: return {256, 256};
     default: return {128, 128};
   }
 }

@@ -154,7 +154,7 @@ def test_batched(ctx, pkg, orc, dtype):
     assert_parity(got.reshape(batch, m, n), want, orc, dtype, ulp_tol=1)
 
 
-@pytest.mark.parametrize("tile", [0, 1, 2, 3, 4, 5])
+@pytest.mark.parametrize("tile", [0, 1, 2, 3, 4, 5, 6])
 @pytest.mark.parametrize("splits", [1, 2, 3, 5])
 def test_forced_tiles_and_splits(ctx, pkg, orc, tile, splits):
     """Every tile shape, with and without split-K (incl. uneven k ranges)."""
@@ -181,7 +181,7 @@ def test_forced_tiles_and_splits(ctx, pkg, orc, tile, splits):
 
 
 @pytest.mark.parametrize("group_m", [1, 3, 5, 8, 1000])
-@pytest.mark.parametrize("tile,splits", [(4, 1), (0, 1), (3, 2), (5, 1)])
+@pytest.mark.parametrize("tile,splits", [(4, 1), (0, 1), (3, 2), (5, 1), (6, 1)])
 def test_tile_enumeration_bands(ctx, pkg, orc, group_m, tile, splits):
     """Every band height of the tile enumeration (including ones that do not
     divide the tile grid, and more than its height) maps blocks onto tiles
