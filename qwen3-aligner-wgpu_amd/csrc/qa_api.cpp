@@ -250,7 +250,8 @@ void choose_group_m(qa::Plan& pl, int64_t span) {
 // for half as many n-tiles as 256 x 128.  Measured on the 300-chunk second
 // level (c = 480): 256 x 128 took 2.07 ms with the whole-range band (118
 // m-tiles, each slab re-fetched once per n-tile) and 1.50 ms with bands of
-// 8; 128 x 256 with the window's band takes 1.37-1.41 ms.
+// 8; 128 x 256 with the window's band takes 1.37-1.41 ms, and 256 x 256 (the
+// modelled choice there) 1.24-1.28 ms.
 qa::Plan plan_conv(int64_t M, int64_t N, int64_t K, bool gelu, int num_cus) {
   qa::Plan pl{};
   pl.epi = gelu ? qa::EPI_GELU : qa::EPI_PLAIN;
