@@ -222,6 +222,47 @@ int qah_aligner_time(qah_aligner* h, int warmup, int steps, int use_graph, doubl
 int qah_aligner_profile(qah_aligner* h, int steps, double* ms);
 void qah_aligner_destroy(qah_aligner* h);
 
+/* ---- the real-checkpoint loader (checkpoint.cpp) ---- */
+/* A Qwen3-ForcedAligner checkpoint directory (src/weights.rs:207-290):
+ * model.safetensors, or model.safetensors.index.json and its shards, mapped
+ * read-only; tensor names of the `-hf` conversion are mapped onto the
+ * original ones (model.language_model. -> thinker.model., model.audio_tower.
+ * -> thinker.audio_tower., model.multi_modal_projector.linear_{1,2} ->
+ * thinker.audio_tower.proj{1,2}, thinker.lm_head. -> score.). */
+typedef struct qah_ckpt qah_ckpt;
+/* The dimensions config.json records, in its original (thinker_config) or
+ * `-hf` (audio_config / text_config) layout, with the reference's defaults
+ * for absent fields (src/config.rs:36-150,186-235). */
+typedef struct qah_ckpt_config {
+  int64_t vocab, hidden, inter, layers, nqh, nkvh, hd;
+  double rms_eps, rope_theta;
+  int64_t d_model, enc_layers, enc_heads, enc_ffn, n_mels, c_conv, n_window, n_window_infer,
+      out_dim;
+  int64_t num_labels, timestamp_token_id, audio_start, audio_end, audio_token;
+  double segment_ms;
+} qah_ckpt_config;
+int qah_ckpt_open(const char* dir, qah_ckpt** out);
+/* The message of the last failing qah_ckpt_* call on this thread. */
+const char* qah_ckpt_error(void);
+/* Tensor metadata: dtype 0 f16, 1 bf16, 2 f32, 3 other; up to 8 dims. */
+int qah_ckpt_tensor(qah_ckpt* c, const char* name, int* dtype, int* ndim, int64_t* shape);
+/* The tensor converted to QA_F16 / QA_BF16 (round to nearest even; a copy
+ * when it is stored so) or to f32; elems must equal its element count. */
+int qah_ckpt_read_h16(qah_ckpt* c, const char* name, int dtype, uint16_t* dst, int64_t elems);
+int qah_ckpt_read_f32(qah_ckpt* c, const char* name, float* dst, int64_t elems);
+int qah_ckpt_read_config(qah_ckpt* c, qah_ckpt_config* out);
+/* Build the aligner from the checkpoint: an audio tower sized for
+ * max_seconds of audio, a decoder of max_rows positions (RoPE tables of
+ * config.json's theta), the embedding and the head.  Linear and conv
+ * weights go to the run's 16-bit format; the decoder's and the tower's norm
+ * weights are rounded to it too (src/decoder.rs:823-826,
+ * src/audio_encoder_gpu.rs:330-331); the final norm and the score head stay
+ * f32 (src/align_inference.rs:405-430).  Absent linear biases read as zero.
+ * On success the caller owns all three (destroy the aligner first). */
+int qah_ckpt_load_aligner(qah_ckpt* c, qa_ctx* ctx, int dtype, double max_seconds, int max_rows,
+                          qah_aenc** enc, qah_tdec** dec, qah_aligner** al);
+void qah_ckpt_close(qah_ckpt* c);
+
 /* Time `iters` back-to-back launches of one descriptor (HIP events around the
  * whole run on the context's stream); ms per launch. */
 int qah_time_linear(qa_ctx* ctx, const qa_linear_desc* desc, int warmup, int iters,

@@ -101,10 +101,124 @@ def declare(L: ctypes.CDLL) -> None:
                  "qah_aenc_set_mel", "qah_aenc_forward", "qah_aenc_read", "qah_aenc_time",
                  "qah_aenc_profile"):
         getattr(L, name).restype = _i
+    L.qah_ckpt_open.argtypes = [ctypes.c_char_p, ctypes.POINTER(_vp)]
+    L.qah_ckpt_error.argtypes = []
+    L.qah_ckpt_error.restype = ctypes.c_char_p
+    L.qah_ckpt_tensor.argtypes = [_vp, ctypes.c_char_p, ctypes.POINTER(_i), ctypes.POINTER(_i),
+                                  ctypes.POINTER(ctypes.c_int64)]
+    L.qah_ckpt_read_h16.argtypes = [_vp, ctypes.c_char_p, _i, _vp, ctypes.c_int64]
+    L.qah_ckpt_read_f32.argtypes = [_vp, ctypes.c_char_p, _vp, ctypes.c_int64]
+    L.qah_ckpt_read_config.argtypes = [_vp, ctypes.POINTER(CkptConfig)]
+    L.qah_ckpt_load_aligner.argtypes = [_vp, _vp, _i, ctypes.c_double, _i] + [ctypes.POINTER(_vp)] * 3
+    L.qah_ckpt_close.argtypes = [_vp]
+    L.qah_ckpt_close.restype = None
+    for name in ("qah_ckpt_open", "qah_ckpt_tensor", "qah_ckpt_read_h16", "qah_ckpt_read_f32",
+                 "qah_ckpt_read_config", "qah_ckpt_load_aligner"):
+        getattr(L, name).restype = _i
 
 
 def _p(a):
     return None if a is None else a.ctypes.data
+
+
+class CkptConfig(ctypes.Structure):
+    """qah_ckpt_config (csrc/host/qa_host.h)."""
+
+    _fields_ = ([(n, ctypes.c_int64) for n in ("vocab", "hidden", "inter", "layers", "nqh", "nkvh", "hd")]
+                + [("rms_eps", ctypes.c_double), ("rope_theta", ctypes.c_double)]
+                + [(n, ctypes.c_int64) for n in ("d_model", "enc_layers", "enc_heads", "enc_ffn",
+                                                 "n_mels", "c_conv", "n_window", "n_window_infer",
+                                                 "out_dim", "num_labels", "timestamp_token_id",
+                                                 "audio_start", "audio_end", "audio_token")]
+                + [("segment_ms", ctypes.c_double)])
+
+
+class CheckpointError(RuntimeError):
+    def __init__(self, code: int, message: str):
+        super().__init__(f"{message} (code {code})")
+        self.code, self.message = code, message
+
+
+def _ck(rc: int) -> None:
+    if rc != 0:
+        raise CheckpointError(rc, host_lib().qah_ckpt_error().decode())
+
+
+class Checkpoint:
+    """qah_ckpt: a Qwen3-ForcedAligner checkpoint directory -- safetensors
+    shards mapped read-only, `-hf` names mapped onto the original ones
+    (src/weights.rs:207-290) -- and the aligner built from it."""
+
+    DTYPES = {0: "F16", 1: "BF16", 2: "F32", 3: "other"}
+
+    def __init__(self, path: str):
+        h = _vp()
+        _ck(host_lib().qah_ckpt_open(str(path).encode(), ctypes.byref(h)))
+        self.handle = h.value
+
+    def close(self):
+        if self.handle:
+            host_lib().qah_ckpt_close(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def tensor(self, name: str):
+        """(dtype name, shape) of a tensor."""
+        dt, nd, shape = _i(), _i(), (ctypes.c_int64 * 8)()
+        _ck(host_lib().qah_ckpt_tensor(self.handle, name.encode(), ctypes.byref(dt),
+                                       ctypes.byref(nd), shape))
+        return self.DTYPES[dt.value], tuple(shape[i] for i in range(nd.value))
+
+    def read_h16(self, name: str, dtype: int) -> np.ndarray:
+        """The tensor in QA_F16 / QA_BF16 bits, in its own shape."""
+        _, shape = self.tensor(name)
+        out = np.empty(shape, np.uint16)
+        _ck(host_lib().qah_ckpt_read_h16(self.handle, name.encode(), dtype, _p(out), out.size))
+        return out
+
+    def read_f32(self, name: str) -> np.ndarray:
+        _, shape = self.tensor(name)
+        out = np.empty(shape, np.float32)
+        _ck(host_lib().qah_ckpt_read_f32(self.handle, name.encode(), _p(out), out.size))
+        return out
+
+    def config(self) -> dict:
+        c = CkptConfig()
+        _ck(host_lib().qah_ckpt_read_config(self.handle, ctypes.byref(c)))
+        return {n: getattr(c, n) for n, _ in CkptConfig._fields_}
+
+    def load_aligner(self, ctx, dtype: int, max_seconds: float, max_rows: int):
+        """(Aligner, AudioEncoder, TextDecoder) loaded from the checkpoint;
+        close the aligner before the other two."""
+        c = self.config()
+        e, d, a = _vp(), _vp(), _vp()
+        _ck(host_lib().qah_ckpt_load_aligner(self.handle, ctx.handle, dtype, max_seconds, max_rows,
+                                             ctypes.byref(e), ctypes.byref(d), ctypes.byref(a)))
+        f = lambda v: (v - 1) // 2 + 1  # noqa: E731
+        cs = 2 * c["n_window"]
+        max_samples = int(max_seconds * 16000)
+        enc = AudioEncoder.__new__(AudioEncoder)
+        enc.ctx, enc.dtype, enc.layers = ctx, dtype, c["enc_layers"]
+        enc.max_chunks = (max_samples // 160 + cs - 1) // cs
+        enc.n_mels, enc.cs, enc.c_conv, enc.d_model = c["n_mels"], cs, c["c_conv"], c["d_model"]
+        enc.nh, enc.ffn, enc.out_dim = c["enc_heads"], c["enc_ffn"], c["out_dim"]
+        enc.wlen = f(f(f(cs))) * c["n_window_infer"] // 100
+        enc.h3, enc.w3 = f(f(f(c["n_mels"]))), f(f(f(cs)))
+        enc.handle = e.value
+        dec = TextDecoder.__new__(TextDecoder)
+        dec.ctx, dec.dtype, dec.layers, dec.max_rows = ctx, dtype, c["layers"], max_rows
+        dec.hidden, dec.nqh, dec.nkvh, dec.hd, dec.inter = (c["hidden"], c["nqh"], c["nkvh"],
+                                                            c["hd"], c["inter"])
+        dec.handle = d.value
+        al = Aligner.__new__(Aligner)
+        al.ctx, al.enc, al.dec, al.vocab, al.labels = ctx, enc, dec, c["vocab"], c["num_labels"]
+        al.handle, al.info = a.value, None
+        return al, enc, dec
 
 
 def synth_normal(seed: int, tensor_id: int, shape, mean: float = 0.0, std: float = 1.0,
