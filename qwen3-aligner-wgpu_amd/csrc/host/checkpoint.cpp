@@ -118,9 +118,14 @@ bool Checkpoint::map_shard(const std::string& path, std::string* err) {
     st_.dtype_name = dt->text;
     st_.dtype = dt->text == "F16" ? ST_F16 : dt->text == "BF16" ? ST_BF16
                 : dt->text == "F32" ? ST_F32 : ST_OTHER;
+    int64_t elems = 1;
     for (const auto& d : sh->items) {
-      if (!d.is_int() || d.as_int() < 0) return *err = path + ": bad shape of " + f.first, false;
-      st_.shape.push_back(d.as_int());
+      const int64_t n = d.is_int() ? d.as_int() : -1;
+      // a dimension past 2^40, or a product past 2^48 elements, is no tensor of a model this size
+      if (n < 0 || n > ((int64_t)1 << 40) || (n && elems > ((int64_t)1 << 48) / n))
+        return *err = path + ": bad shape of " + f.first, false;
+      elems *= n;
+      st_.shape.push_back(n);
     }
     const uint64_t o0 = off->items[0].as_uint(), o1 = off->items[1].as_uint();
     if (o0 > o1 || o1 > dlen) return *err = path + ": data of " + f.first + " out of range", false;
