@@ -140,7 +140,7 @@ double stage_us(int tile) {
     case qa::TILE_128x256: return 0.95;
     case qa::TILE_128x192: return 0.72;
     case qa::TILE_64x128: return 0.36;
-    case qa::TILE_64x64: return 0.27;
+    case qa::TILE_64x64: return 0.25;
     case qa::TILE_256x256: return 1.75;
     default: return 0.56;
   }

@@ -21,7 +21,7 @@ enum TileCfg : int {
   TILE_256x128 = 1,  // waves of 128(m) x 64(n)
   TILE_128x256 = 2,  // waves of 64(m) x 128(n)
   TILE_64x128 = 3,   // waves of 32(m) x 64(n)
-  TILE_64x64 = 4,    // waves of 32x32
+  TILE_64x64 = 4,    // waves of 32(m) x 64(n)
   TILE_128x192 = 5,  // waves of 64(m) x 96(n)
   TILE_256x256 = 6,  // one k group of 2x4 waves of 128(m) x 64(n)
   TILE_COUNT
