@@ -158,13 +158,13 @@ __global__ void __launch_bounds__(256) qk_norm_rope_kernel(const RopeParams p) {
 // arithmetic per element is qk_norm_rope_kernel's; only the order of the
 // sum of squares differs.
 template <int DT>
-__global__ void __launch_bounds__(256) qk_norm_rope_vec_kernel(const RopeParams p) {
+__device__ __forceinline__ void qk_norm_rope_vec_body(const RopeParams& p, int64_t bx) {
   const int lane = threadIdx.x & 63;
   const int L = p.hd >> 4;  // lanes per head: 4, 8 or 16
   const int hpw = 64 / L;   // head slots per wave
   const int slots = p.nqh + p.nkvh;
   const int groups = (slots + hpw - 1) / hpw;
-  const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t item = bx * 4 + (threadIdx.x >> 6);
   if (item >= p.rows * groups) return;
   const int64_t r = item / groups;
   const int slot = (int)(item % groups) * hpw + lane / L;
@@ -252,11 +252,11 @@ __device__ __forceinline__ int64_t vperm(int64_t t) {
 // 64 (rows) x 64 (d) LDS tile, so the row reads are contiguous and the
 // transposed writes stay within 32-byte groups.
 template <int DT>
-__global__ void __launch_bounds__(256) v_transpose_kernel(const RopeParams p) {
+__device__ __forceinline__ void v_transpose_body(const RopeParams& p, int64_t bx, int by, int bz) {
   __shared__ uint16_t tile[64][66];
-  const int64_t r0 = (int64_t)blockIdx.x * 64;
-  const int d0 = blockIdx.y * 64;
-  const int h = blockIdx.z;
+  const int64_t r0 = bx * 64;
+  const int d0 = by * 64;
+  const int h = bz;
   const int t = threadIdx.x;
   const uint16_t* v = p.qkv + (int64_t)(p.nqh + p.nkvh) * p.hd + (int64_t)h * p.hd + d0;
   {
@@ -292,6 +292,27 @@ __global__ void __launch_bounds__(256) v_transpose_kernel(const RopeParams p) {
   }
 }
 
+template <int DT>
+__global__ void __launch_bounds__(256) v_transpose_kernel(const RopeParams p) {
+  v_transpose_body<DT>(p, blockIdx.x, blockIdx.y, blockIdx.z);
+}
+
+// Both passes in one grid: blocks [0, nvt) are V-transpose tiles (row tile
+// fastest, then d tile, then kv head), the rest are 16-byte q/k blocks.  The
+// two write disjoint buffers and read only qkv, so they run concurrently and
+// share the HBM stream instead of running one after the other.
+template <int DT>
+__global__ void __launch_bounds__(256) qk_rope_v_kernel(const RopeParams p, int vtx, int vty,
+                                                         int64_t nvt) {
+  const int64_t b = blockIdx.x;
+  if (b < nvt) {
+    const int64_t per_head = (int64_t)vtx * vty;
+    v_transpose_body<DT>(p, b % vtx, (int)((b % per_head) / vtx), (int)(b / per_head));
+  } else {
+    qk_norm_rope_vec_body<DT>(p, b - nvt);
+  }
+}
+
 }  // namespace
 
 hipError_t launch_rms_norm(int dtype, const RmsParams& p, hipStream_t s) {
@@ -322,13 +343,20 @@ hipError_t launch_qk_norm_rope(int dtype, const RopeParams& p, hipStream_t s) {
   const int64_t items = vec ? p.rows * ((slots + 1024 / p.hd - 1) / (1024 / p.hd))
                             : p.rows * slots;
   const dim3 grid((unsigned)((items + 3) / 4));
+  if (vec) {
+    const int64_t nvt = (int64_t)vt.x * vt.y * vt.z;
+    const dim3 fused((unsigned)(nvt + grid.x));
+    if (dtype == QA_BF16)
+      hipLaunchKernelGGL(qk_rope_v_kernel<QA_BF16>, fused, dim3(256), 0, s, p, (int)vt.x, (int)vt.y, nvt);
+    else
+      hipLaunchKernelGGL(qk_rope_v_kernel<QA_F16>, fused, dim3(256), 0, s, p, (int)vt.x, (int)vt.y, nvt);
+    return hipGetLastError();
+  }
   if (dtype == QA_BF16) {
-    if (vec) hipLaunchKernelGGL(qk_norm_rope_vec_kernel<QA_BF16>, grid, dim3(256), 0, s, p);
-    else hipLaunchKernelGGL(qk_norm_rope_kernel<QA_BF16>, grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL(qk_norm_rope_kernel<QA_BF16>, grid, dim3(256), 0, s, p);
     hipLaunchKernelGGL(v_transpose_kernel<QA_BF16>, vt, dim3(256), 0, s, p);
   } else {
-    if (vec) hipLaunchKernelGGL(qk_norm_rope_vec_kernel<QA_F16>, grid, dim3(256), 0, s, p);
-    else hipLaunchKernelGGL(qk_norm_rope_kernel<QA_F16>, grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL(qk_norm_rope_kernel<QA_F16>, grid, dim3(256), 0, s, p);
     hipLaunchKernelGGL(v_transpose_kernel<QA_F16>, vt, dim3(256), 0, s, p);
   }
   return hipGetLastError();
