@@ -65,37 +65,59 @@ __global__ void __launch_bounds__(256) mel_log_kernel(const MelParams p) {
     xw[j][f] = v;
   }
   __syncthreads();
-  // one thread per bin k: the 16 frames' DFT at k
-  if (tid < NBIN) {
-    const int k = tid;
+  // One radix-2 split of the real 400-point DFT.  For bin k = 0..100, lanes
+  // 0-31 of a wave sum the even samples (E[k], a 200-point DFT) and lanes
+  // 32-63 the odd ones (O[k]) of the same 32 bins; then X[k] = E + w^k O and,
+  // since E and O of real input satisfy E[200 - k] = conj(E[k]) (same for O)
+  // and w^(200 - k) = -conj(w^k), |X[200 - k]| = |E[k] - w^k O[k]|.
+  {
+    const int lane = tid & 63, half = lane >> 5;
+    const int k = (tid >> 6) * 32 + (lane & 31);
+    const bool act = k <= NFFT / 4;
     double re[FB], im[FB];
 #pragma unroll
     for (int f = 0; f < FB; ++f) re[f] = im[f] = 0.0;
-    const double rr = tc[k], ri = -ts[k];  // e^{-2 pi i k / 400}
-    double wr = 1.0, wi = 0.0;
-    for (int j0 = 0; j0 < NFFT; j0 += kAnchor) {
-      const int idx = (j0 * k) % NFFT;
-      wr = tc[idx];
-      wi = -ts[idx];
-      for (int j = j0; j < j0 + kAnchor; ++j) {
-        typedef float f32x4 __attribute__((ext_vector_type(4)));
-        const f32x4* row = reinterpret_cast<const f32x4*>(&xw[j][0]);
+    if (act) {
+      const int step = (2 * k) % NFFT;
+      const double rr = tc[step], ri = -ts[step];  // e^{-2 pi i 2k / 400}
+      for (int n0 = 0; n0 < NFFT / 2; n0 += kAnchor) {
+        const int idx = (2 * n0 * k) % NFFT;
+        double wr = tc[idx], wi = -ts[idx];
+        for (int n = n0; n < n0 + kAnchor; ++n) {
+          typedef float f32x4 __attribute__((ext_vector_type(4)));
+          const f32x4* row = reinterpret_cast<const f32x4*>(&xw[2 * n + half][0]);
 #pragma unroll
-        for (int q = 0; q < FB / 4; ++q) {
-          const f32x4 x4 = row[q];
+          for (int q = 0; q < FB / 4; ++q) {
+            const f32x4 x4 = row[q];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            re[4 * q + e] += (double)x4[e] * wr;
-            im[4 * q + e] += (double)x4[e] * wi;
+            for (int e = 0; e < 4; ++e) {
+              re[4 * q + e] += (double)x4[e] * wr;
+              im[4 * q + e] += (double)x4[e] * wi;
+            }
           }
+          const double nr = wr * rr - wi * ri;
+          wi = wr * ri + wi * rr;
+          wr = nr;
         }
-        const double nr = wr * rr - wi * ri;
-        wi = wr * ri + wi * rr;
-        wr = nr;
       }
     }
+    double ore[FB], oim[FB];  // the odd half's sums, in the even lanes
 #pragma unroll
-    for (int f = 0; f < FB; ++f) pw[f][k] = (float)(re[f] * re[f] + im[f] * im[f]);
+    for (int f = 0; f < FB; ++f) {
+      ore[f] = __shfl_xor(re[f], 32, 64);
+      oim[f] = __shfl_xor(im[f], 32, 64);
+    }
+    if (act && half == 0) {
+      const double cr = tc[k], ci = -ts[k];  // w^k = e^{-2 pi i k / 400}
+#pragma unroll
+      for (int f = 0; f < FB; ++f) {
+        const double tr = cr * ore[f] - ci * oim[f], ti = cr * oim[f] + ci * ore[f];
+        const double ar = re[f] + tr, ai = im[f] + ti;
+        const double br = re[f] - tr, bi = im[f] - ti;
+        pw[f][k] = (float)(ar * ar + ai * ai);
+        if (k != NFFT / 4) pw[f][NFFT / 2 - k] = (float)(br * br + bi * bi);
+      }
+    }
   }
   __syncthreads();
   // mel m of the 16 frames: sum_k filt[m][k] pw[f][k] in k order, skipping the
