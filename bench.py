@@ -166,15 +166,6 @@ def bench_decoder(pkg, host, ctx, m, warmup, steps, tdec=None):
     return dec, ev_ms, wall_ms, sites
 
 
-def rope_tables(positions, hd, theta=1e6):
-    """Text-position RoPE tables cos/sin [positions][hd] (src/mrope.rs:55-82)."""
-    half = hd // 2
-    inv = 1.0 / theta ** (2.0 * np.arange(half) / hd)
-    ang = np.arange(positions, dtype=np.float64)[:, None] * inv[None, :]
-    return (np.concatenate([np.cos(ang)] * 2, axis=1).astype(np.float32),
-            np.concatenate([np.sin(ang)] * 2, axis=1).astype(np.float32))
-
-
 def dec_layer_flops(s):
     """Per-layer FLOPs of a prefill of s tokens: the four projections plus the
     causal attention (QK^T and PV over the s(s+1)/2 visible pairs per head)."""
@@ -376,7 +367,7 @@ def main():
     if not args.no_detail:
         tdec = host.TextDecoder(ctx, pkg.F16, DEC["layers"], max(PREFILL_ROWS), DEC["hidden"],
                                 DEC["nqh"], DEC["nkvh"], DEC["hd"], DEC["inter"])
-        tdec.set_rope(*rope_tables(max(PREFILL_ROWS), DEC["hd"]))
+        tdec.set_rope(*pkg.rope_tables(max(PREFILL_ROWS), DEC["hd"], 1e6, pkg.F16))
     dec, ev_ms, wall_ms, sites = bench_decoder(pkg, host, ctx, m, args.warmup, args.steps, tdec)
     ms_per_step = max(ev_ms, wall_ms)
     value = total_flops / (ms_per_step * 1e-3) / 1e12

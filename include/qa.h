@@ -370,9 +370,15 @@ int qa_log_mel(qa_ctx* ctx, const qa_mel_desc* desc);
 
 /* RoPE tables for text positions 0..positions-1 (all three M-RoPE axes equal,
  * as the aligner prefills them, src/mrope.rs:55-89 with text_positions):
- * angle(p, j) = p / theta^(2j / hd) in f64, cos / sin [positions][hd] f32,
- * the second half repeating the first.  Host function, no device needed. */
-int qa_rope_tables(int64_t positions, int hd, double theta, float* cos_out, float* sin_out);
+ * angle(p, j) = p / theta^(2j / hd) in f64, cos / sin rounded to f32 and then
+ * to the run's 16-bit format `dtype` (QA_F16 / QA_BF16), as the reference
+ * narrows both tables before either decoder reads them
+ * (src/align_inference.rs:371-372 on the GPU path, :394-395 on the CPU path,
+ * src/cpu_decoder.rs:247); stored widened back to f32 [positions][hd], the
+ * second half repeating the first.  The aligner uses theta = 1e6
+ * (src/align_inference.rs:322-327).  Host function, no device needed. */
+int qa_rope_tables(int64_t positions, int hd, double theta, uint32_t dtype, float* cos_out,
+                   float* sin_out);
 
 /* The decoder's input rows: out[r] = table[src[r]] (the token embedding) for
  * src[r] >= 0 and audio[-src[r] - 1] (the audio tower's output row) for

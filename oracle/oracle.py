@@ -108,6 +108,18 @@ def lib() -> ctypes.CDLL:
         L.or_log_mel.restype = None
         L.or_timestamp_head.argtypes = [ci, i64, p, p, i64, i64, p, f, p, i64, p, p]
         L.or_timestamp_head.restype = None
+        L.or_linear_f32.argtypes = [i64, i64, i64, p, i64, p, ci, p, p, i64]
+        L.or_linear_f32.restype = None
+        L.or_layer_norm_f32.argtypes = [i64, i64, p, p, p, f, p]
+        L.or_layer_norm_f32.restype = None
+        L.or_gelu_f32_n.argtypes = [p, i64]
+        L.or_gelu_f32_n.restype = None
+        L.or_window_attention_f32.argtypes = [i64, ci, ci, i64, p, p, p, i64, p]
+        L.or_window_attention_f32.restype = None
+        L.or_conv3x3s2_f32.argtypes = [i64, i64, i64, i64, i64, p, p, i64, p, ci, ci, p]
+        L.or_conv3x3s2_f32.restype = None
+        L.or_head_fold.argtypes = [ci, i64, p, p, i64, i64, p, f, p]
+        L.or_head_fold.restype = None
         L.or_vperm.restype = i64
         L.or_num_threads.restype = ctypes.c_int
         L.or_set_threads.argtypes = [ci]
@@ -364,6 +376,86 @@ def timestamp_head(dtype: int, h: np.ndarray, positions, w: np.ndarray, eps: flo
                             _ptr(_c(w, np.float32)), ctypes.c_float(eps), _ptr(score), labels,
                             _ptr(logits), _ptr(cls))
     return logits, cls
+
+
+# ---- the reference's CPU audio tower in f32 (CpuAudioEncoder::forward) ----
+
+def linear_f32(x: np.ndarray, w: np.ndarray, dtype: int, bias: np.ndarray | None = None) -> np.ndarray:
+    """or_linear_f32: f32 x [m, k] . (16-bit W [n, k] widened)^T, + f32 bias -> f32 [m, n]."""
+    x = _c(x, np.float32)
+    w = _c(w, np.uint16)
+    m, k = x.shape
+    n = w.shape[0]
+    y = np.empty((m, n), np.float32)
+    bb = _c(bias, np.float32) if bias is not None else None
+    lib().or_linear_f32(m, n, k, _ptr(x), k, _ptr(w), dtype, _ptr(bb) if bb is not None else None,
+                        _ptr(y), n)
+    return y
+
+
+def layer_norm_f32(x: np.ndarray, w: np.ndarray, b: np.ndarray, eps: float) -> np.ndarray:
+    """or_layer_norm_f32: f32 rows -> f32 rows."""
+    x = _c(x, np.float32)
+    y = np.empty_like(x)
+    lib().or_layer_norm_f32(x.shape[0], x.shape[1], _ptr(x), _ptr(_c(w, np.float32)),
+                            _ptr(_c(b, np.float32)), ctypes.c_float(eps), _ptr(y))
+    return y
+
+
+def gelu_f32(x: np.ndarray) -> np.ndarray:
+    """or_gelu_f32_n: elementwise erf GELU in f32 (a new array)."""
+    y = _c(x, np.float32).copy()
+    lib().or_gelu_f32_n(_ptr(y), y.size)
+    return y
+
+
+def window_attention_f32(q: np.ndarray, k: np.ndarray, v: np.ndarray, nh: int, hd: int,
+                         wlen: int) -> np.ndarray:
+    """or_window_attention_f32: f32 q, k, v [s, nh*hd] -> out [s, nh*hd] f32."""
+    q, k, v = (_c(a, np.float32) for a in (q, k, v))
+    s = q.shape[0]
+    out = np.empty((s, nh * hd), np.float32)
+    lib().or_window_attention_f32(s, nh, hd, wlen, _ptr(q), _ptr(k), _ptr(v), q.shape[1], _ptr(out))
+    return out
+
+
+def conv3x3s2_f32(x: np.ndarray, weight: np.ndarray, bias: np.ndarray | None, *,
+                  gelu: bool = True, token_major: bool = False) -> np.ndarray:
+    """or_conv3x3s2_f32: x [b, h, w, c_in] f32, weight [c_out, ldw] f32
+    (k = (kh*3+kw)*c_in+ic), bias [c_out] f32 or None -> y [b*ho*wo, c_out] f32."""
+    x = _c(x, np.float32)
+    weight = _c(weight, np.float32)
+    b, h, w, c_in = x.shape
+    c_out, ldw = weight.shape
+    ho, wo = (h - 1) // 2 + 1, (w - 1) // 2 + 1
+    y = np.empty((b * ho * wo, c_out), np.float32)
+    bb = _c(bias, np.float32) if bias is not None else None
+    lib().or_conv3x3s2_f32(b, h, w, c_in, c_out, _ptr(x), _ptr(weight), ldw,
+                           _ptr(bb) if bb is not None else None, int(gelu), int(token_major),
+                           _ptr(y))
+    return y
+
+
+def head_fold(dtype: int, h: np.ndarray, positions, w: np.ndarray, eps: float) -> np.ndarray:
+    """or_head_fold: the folded final norm of rows `positions` of h -> f32 [rows, n]."""
+    h = _c(h, np.uint16)
+    pos = _c(np.asarray(positions), np.int32)
+    n = h.shape[1]
+    y = np.empty((pos.size, n), np.float32)
+    lib().or_head_fold(dtype, pos.size, _ptr(pos), _ptr(h), n, n, _ptr(_c(w, np.float32)),
+                       ctypes.c_float(eps), _ptr(y))
+    return y
+
+
+def timestamp_head_f32(dtype: int, h: np.ndarray, positions, w: np.ndarray, eps: float,
+                       score: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """The head as the reference computes it on the host
+    (src/align_inference.rs:766-805): the folded norm in f32, the logits with
+    the f32 GEMM (cpu_tensor::linear -> or_gemm_f32), the first index of the
+    maximum -> (logits f32 [rows, labels], classes int32 [rows])."""
+    y = head_fold(dtype, h, positions, w, eps)
+    logits = gemm_f32(y, _c(score, np.float32))
+    return logits, np.argmax(logits, axis=1).astype(np.int32)
 
 
 def fix_timestamps(data) -> list[int]:

@@ -148,6 +148,26 @@ void or_timestamp_head(int dtype, int64_t rows, const int32_t* pos, const uint16
                        int64_t ldh, int64_t n, const float* w, float eps, const float* score,
                        int64_t labels, double* logits, int32_t* cls);
 
+/* The reference's CPU audio tower in f32 throughout (CpuAudioEncoder::forward,
+ * src/audio_encoder.rs:754-832; one f16 narrowing at the end,
+ * src/align_inference.rs:124-131).  Pins (tests/test_oracle_audio.py): each
+ * equals its 16-bit twin above on inputs that are 16-bit values, up to that
+ * twin's final rounding; f64 closed forms (LayerNorm, attention, conv against
+ * torch conv2d); the linear against numpy f64 matmul + bias. */
+void or_linear_f32(int64_t m, int64_t n, int64_t k, const float* x, int64_t ldx,
+                   const uint16_t* w, int dtype, const float* bias, float* y, int64_t ldy);
+void or_layer_norm_f32(int64_t rows, int64_t n, const float* x, const float* w, const float* b,
+                       float eps, float* y);
+void or_gelu_f32_n(float* x, int64_t n);
+void or_window_attention_f32(int64_t s, int nh, int hd, int64_t wlen, const float* q,
+                             const float* k, const float* v, int64_t ld, float* out);
+void or_conv3x3s2_f32(int64_t batch, int64_t h, int64_t w, int64_t c_in, int64_t c_out,
+                      const float* x, const float* weight, int64_t ldw, const float* bias,
+                      int gelu, int tmajor, float* y);
+/* The head's folded norm alone, f32 rows y [rows][n] (src/align_inference.rs:766-783). */
+void or_head_fold(int dtype, int64_t rows, const int32_t* pos, const uint16_t* h, int64_t ldh,
+                  int64_t n, const float* w, float eps, float* y);
+
 #ifdef __cplusplus
 }
 #endif

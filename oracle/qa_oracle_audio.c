@@ -295,3 +295,151 @@ void or_timestamp_head(int dtype, int64_t rows, const int32_t* pos, const uint16
     free(y);
   }
 }
+
+/* ---- The CPU tower of the reference, in f32 throughout -------------------
+ * CpuAudioEncoder::forward (src/audio_encoder.rs:754-832) keeps every value of
+ * the tower in f32: its linears add an f32 bias to an f32 GEMM
+ * (CpuAudioLinear::forward, :134-143), the residual adds and GELUs are f32
+ * (:672-689, :194-202), and only the output is narrowed, once, to f16
+ * (src/align_inference.rs:124-131).  The functions below restate those ops
+ * on f32 buffers; tests/chains.py composes them into that forward.  (The
+ * functions above take and return the GPU tower's 16-bit buffers instead.) */
+
+/* CpuAudioLinear::forward: y = x . W^T with the f32 GEMM (or_gemm_f32, the
+ * gemm crate restatement), then y[j] += b[j] in f32.  W is the f16 (or bf16)
+ * checkpoint matrix [n][k] widened once, as CpuWeightF16::to_f32 does. */
+void or_linear_f32(int64_t m, int64_t n, int64_t k, const float* x, int64_t ldx,
+                   const uint16_t* w, int dtype, const float* bias, float* y, int64_t ldy) {
+  float* wf = (float*)malloc((size_t)(n * k) * sizeof(float));
+  or_h16_to_f32_n(w, wf, n * k, dtype);
+  or_gemm_f32(m, n, k, x, ldx, wf, k, y, ldy, 0.0f);
+  free(wf);
+  if (!bias) return;
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < m; ++i)
+    for (int64_t j = 0; j < n; ++j) y[i * ldy + j] += bias[j];
+}
+
+/* CpuAudioLayerNorm::forward on f32 rows (the same sums as or_layer_norm). */
+void or_layer_norm_f32(int64_t rows, int64_t n, const float* x, const float* w, const float* b,
+                       float eps, float* y) {
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < rows; ++r) {
+    const float* xr = x + r * n;
+    float mean = 0.f;
+    for (int64_t j = 0; j < n; ++j) mean += xr[j];
+    mean /= (float)n;
+    float var = 0.f;
+    for (int64_t j = 0; j < n; ++j) {
+      const float d = xr[j] - mean;
+      var += d * d;
+    }
+    var /= (float)n;
+    const float inv_std = 1.0f / sqrtf(var + eps);
+    for (int64_t j = 0; j < n; ++j) y[r * n + j] = (xr[j] - mean) * inv_std * w[j] + b[j];
+  }
+}
+
+/* gelu_inplace (src/audio_encoder.rs:194-202). */
+void or_gelu_f32_n(float* x, int64_t n) {
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < n; ++i) x[i] = or_gelu(x[i]);
+}
+
+/* attention_window over every window (CpuAudioAttention::flat,
+ * src/audio_encoder.rs:493-616) on f32 q, k, v rows [s][ld] (the separate
+ * q_proj / k_proj / v_proj outputs; head h at columns h*hd): the arithmetic
+ * of or_window_attention without the 16-bit widening and rounding.  out
+ * [s][nh*hd] (the [b, s, nh*hd] flat layout). */
+void or_window_attention_f32(int64_t s, int nh, int hd, int64_t wlen, const float* q,
+                             const float* k, const float* v, int64_t ld, float* out) {
+  const float scale = 1.0f / sqrtf((float)hd);
+  const int64_t nwin = (s + wlen - 1) / wlen, dm = (int64_t)nh * hd;
+#pragma omp parallel for collapse(2) schedule(dynamic)
+  for (int64_t wi = 0; wi < nwin; ++wi)
+    for (int h = 0; h < nh; ++h) {
+      const int64_t st = wi * wlen;
+      const int64_t len = (st + wlen <= s) ? wlen : s - st;
+      float* sc = (float*)malloc((size_t)len * sizeof(float));
+      for (int64_t qi = 0; qi < len; ++qi) {
+        const float* qr = q + (st + qi) * ld + (int64_t)h * hd;
+        float mx = -INFINITY;
+        for (int64_t ki = 0; ki < len; ++ki) {
+          const float* kr = k + (st + ki) * ld + (int64_t)h * hd;
+          float dot = 0.f;
+          for (int j = 0; j < hd; ++j) dot += qr[j] * kr[j];
+          sc[ki] = dot * scale;
+          if (sc[ki] > mx) mx = sc[ki];
+        }
+        float sum = 0.f;
+        for (int64_t ki = 0; ki < len; ++ki) {
+          sc[ki] = expf(sc[ki] - mx);
+          sum += sc[ki];
+        }
+        const float inv = 1.0f / sum;
+        float* o = out + (st + qi) * dm + (int64_t)h * hd;
+        for (int j = 0; j < hd; ++j) o[j] = 0.f;
+        for (int64_t ki = 0; ki < len; ++ki) {
+          const float wgt = sc[ki] * inv;
+          const float* vr = v + (st + ki) * ld + (int64_t)h * hd;
+          for (int j = 0; j < hd; ++j) o[j] += wgt * vr[j];
+        }
+      }
+      free(sc);
+    }
+}
+
+/* CpuConvStem::conv_block on f32 (src/audio_encoder.rs:376-447): 3x3,
+ * stride 2, pad 1, bias, erf GELU, no rounding.  The layouts are the GPU
+ * tower's (x [batch][h][w][c_in], weight [c_out][ldw] with k = (kh*3+kw)*c_in
+ * + ic, rows (b, ho, wo), or (b, wo, ho) when `tmajor`); the sum is
+ * accumulated in f64 and rounded to f32 once, the value the reference's f32
+ * im2col GEMM approximates in its own (unpinned) order.  x and weight are f32
+ * (the weight the widened f16 checkpoint values, CpuWeightF16::to_f32). */
+void or_conv3x3s2_f32(int64_t batch, int64_t h, int64_t w, int64_t c_in, int64_t c_out,
+                      const float* x, const float* weight, int64_t ldw, const float* bias,
+                      int gelu, int tmajor, float* y) {
+  const int64_t ho = (h - 1) / 2 + 1, wo = (w - 1) / 2 + 1, plane = ho * wo;
+  const int64_t M = batch * plane;
+#pragma omp parallel for schedule(dynamic, 4)
+  for (int64_t m = 0; m < M; ++m) {
+    const int64_t b = m / plane, q = m % plane;
+    const int64_t oh = tmajor ? q % ho : q / wo;
+    const int64_t ow = tmajor ? q / ho : q % wo;
+    for (int64_t oc = 0; oc < c_out; ++oc) {
+      const float* wr = weight + oc * ldw;
+      double acc = 0.0;
+      for (int kh = 0; kh < 3; ++kh)
+        for (int kw = 0; kw < 3; ++kw) {
+          const int64_t ih = 2 * oh + kh - 1, iw = 2 * ow + kw - 1;
+          if (ih < 0 || ih >= h || iw < 0 || iw >= w) continue;
+          const float* xp = x + ((b * h + ih) * w + iw) * c_in;
+          const float* wp = wr + (kh * 3 + kw) * c_in;
+          for (int64_t ic = 0; ic < c_in; ++ic) acc += (double)xp[ic] * (double)wp[ic];
+        }
+      float v = (float)acc;
+      if (bias) v += bias[oc];
+      if (gelu) v = or_gelu(v);
+      y[m * c_out + oc] = v;
+    }
+  }
+}
+
+/* The head's folded final norm alone (src/align_inference.rs:766-783), f32:
+ * acc = sum (x w)^2 in order, inv = 1 / sqrt(acc / n + eps), y = x w inv,
+ * for rows pos[r] of h.  y [rows][n]; the reference then multiplies y by the
+ * score matrix with the f32 cpu_tensor::linear (:786-790). */
+void or_head_fold(int dtype, int64_t rows, const int32_t* pos, const uint16_t* h, int64_t ldh,
+                  int64_t n, const float* w, float eps, float* y) {
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < rows; ++r) {
+    const uint16_t* x = h + (int64_t)pos[r] * ldh;
+    float acc = 0.f;
+    for (int64_t j = 0; j < n; ++j) {
+      const float v = or_h16_to_f32(x[j], dtype) * w[j];
+      acc += v * v;
+    }
+    const float inv = 1.0f / sqrtf(acc / (float)n + eps);
+    for (int64_t j = 0; j < n; ++j) y[r * n + j] = or_h16_to_f32(x[j], dtype) * w[j] * inv;
+  }
+}

@@ -315,7 +315,7 @@ def lib() -> ctypes.CDLL:
         L.qa_conv2d_3x3s2.argtypes = [vp, ctypes.POINTER(ConvDesc)]
         L.qa_mel_filterbank.argtypes = [i, i, i, vp]
         L.qa_log_mel.argtypes = [vp, ctypes.POINTER(MelDesc)]
-        L.qa_rope_tables.argtypes = [ctypes.c_int64, i, ctypes.c_double, vp, vp]
+        L.qa_rope_tables.argtypes = [ctypes.c_int64, i, ctypes.c_double, ctypes.c_uint32, vp, vp]
         L.qa_embed_scatter.argtypes = [vp, ctypes.POINTER(EmbedDesc)]
         L.qa_timestamp_head.argtypes = [vp, ctypes.POINTER(HeadDesc)]
         L.qa_last_error.restype = ctypes.c_char_p
@@ -458,11 +458,13 @@ def mel_filterbank(n_mels: int = 128, n_fft: int = 400, sample_rate: int = 16000
     return out
 
 
-def rope_tables(positions: int, hd: int = 128, theta: float = 1e6) -> tuple[np.ndarray, np.ndarray]:
-    """qa_rope_tables (host): cos, sin [positions, hd] f32 for text positions."""
+def rope_tables(positions: int, hd: int = 128, theta: float = 1e6,
+                dtype: int = F16) -> tuple[np.ndarray, np.ndarray]:
+    """qa_rope_tables (host): cos, sin [positions, hd] for text positions,
+    rounded to the run's 16-bit format `dtype` and widened back to f32."""
     c = np.empty((positions, hd), np.float32)
     s = np.empty((positions, hd), np.float32)
-    check(lib().qa_rope_tables(positions, hd, theta, c.ctypes.data, s.ctypes.data))
+    check(lib().qa_rope_tables(positions, hd, theta, dtype, c.ctypes.data, s.ctypes.data))
     return c, s
 
 

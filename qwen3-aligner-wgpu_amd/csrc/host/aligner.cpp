@@ -109,15 +109,19 @@ int Aligner::load_head(const float* w, const float* s) {
 
 int Aligner::prepare(const float* x, int64_t n, int n_words, const int32_t* word_lens,
                      const int32_t* word_ids) {
+  // Forget the previous clip first: after a failed prepare, forward() must
+  // refuse (seq == 0) instead of aligning the old input, and info / the host
+  // arrays must describe nothing rather than a mix of two clips.
+  seq = n_audio = n_ts = 0;
+  ids.clear();
+  src_host.clear();
+  ts_host.clear();
   if (!x || n < kHop || n > max_samples || n_words < 0 || (n_words && (!word_lens || !word_ids)))
     return QA_EINVAL;
   const int64_t frames = n / kHop;  // valid_mel_frames (src/align_input.rs:94-101)
   const int chunks = (int)((frames + enc->cs - 1) / enc->cs);
   const int tl = (int)(frames % enc->cs);
   const int64_t na = enc->tokens(chunks, tl);  // audio_token_count (src/align_input.rs:66-71)
-  ids.clear();
-  src_host.clear();
-  ts_host.clear();
   ids.push_back(tok.audio_start);
   for (int64_t k = 0; k < na; ++k) ids.push_back(tok.audio_pad);
   ids.push_back(tok.audio_end);
@@ -141,10 +145,17 @@ int Aligner::prepare(const float* x, int64_t n, int n_words, const int32_t* word
   // the row source of each position: a token id, or -1 - k for audio row k
   int64_t k = 0;
   for (int32_t id : ids) src_host.push_back(id == tok.audio_pad ? (int32_t)(-1 - k++) : id);
-  if (int rc = qa_upload(ctx, samples.ptr, 0, x, (size_t)n * 4)) return rc;
-  if (int rc = qa_upload(ctx, src.ptr, 0, src_host.data(), src_host.size() * 4)) return rc;
+  auto forget = [&](int rc) {
+    ids.clear();
+    src_host.clear();
+    ts_host.clear();
+    return rc;
+  };
+  if (int rc = qa_upload(ctx, samples.ptr, 0, x, (size_t)n * 4)) return forget(rc);
+  if (int rc = qa_upload(ctx, src.ptr, 0, src_host.data(), src_host.size() * 4)) return forget(rc);
   if (!ts_host.empty())
-    if (int rc = qa_upload(ctx, ts_pos.ptr, 0, ts_host.data(), ts_host.size() * 4)) return rc;
+    if (int rc = qa_upload(ctx, ts_pos.ptr, 0, ts_host.data(), ts_host.size() * 4))
+      return forget(rc);
   n_samples = n;
   seq = s;
   n_audio = na;

@@ -12,6 +12,7 @@
 #include <set>
 #include <sstream>
 
+#include "../half_bits.h"
 #include "json_lite.hpp"
 #include "qa.h"
 
@@ -37,17 +38,17 @@ bool file_exists(const std::string& path) {
 
 int elem_size(int dt) { return dt == ST_F32 ? 4 : (dt == ST_OTHER ? 0 : 2); }
 
-// The 16-bit formats, round to nearest even.  f32 -> f16 through the
-// compiler's IEEE conversion; f32 -> bf16 is the reference's
+// The 16-bit formats, round to nearest even.  f32 -> f16 by integer
+// arithmetic (half_bits.h); f32 -> bf16 is the reference's
 // (u + 0x7fff + ((u >> 16) & 1)) >> 16 (src/shaders.rs:169-179), with NaN
 // kept a quiet NaN.
-uint16_t to_f16(float v) { return __builtin_bit_cast(uint16_t, (_Float16)v); }
+uint16_t to_f16(float v) { return qa_half::f16_from_f32(v); }
 uint16_t to_bf16(float v) {
   const uint32_t u = __builtin_bit_cast(uint32_t, v);
   if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
   return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
 }
-float from_f16(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+float from_f16(uint16_t h) { return qa_half::f16_to_f32(h); }
 float from_bf16(uint16_t h) { return __builtin_bit_cast(float, (uint32_t)h << 16); }
 
 float load_elem(const uint8_t* p, int dt) {
@@ -334,12 +335,37 @@ struct Loader {
 
 }  // namespace
 
+int tower_geometry(const qah_ckpt_config& c, double max_seconds, Geometry* g, std::string* err) {
+  if (!(max_seconds > 0)) return *err = "max_seconds must be > 0", QA_EINVAL;
+  // geometry the tower's kernels and the window formula need (a zero or
+  // negative n_window would divide by zero below)
+  if (c.n_window <= 0 || c.n_mels <= 0 || c.n_window_infer <= 0)
+    return *err = "n_window, n_mels and n_window_infer must be positive", QA_EINVAL;
+  if (c.n_window_infer < 2 * c.n_window)
+    return *err = "n_window_infer is shorter than one chunk (2 n_window frames)", QA_EINVAL;
+  if (c.hd != 128) return *err = "decoder heads must be 128 wide", QA_EUNSUPPORTED;
+  if (c.nqh <= 0 || c.nkvh <= 0 || c.nqh % c.nkvh)
+    return *err = "num_attention_heads must be a positive multiple of num_key_value_heads", QA_EINVAL;
+  if (c.nqh / c.nkvh > 2)
+    return *err = "GQA ratio num_attention_heads / num_key_value_heads above 2", QA_EUNSUPPORTED;
+  g->cs = 2 * c.n_window;  // frames per chunk (src/audio_encoder.rs:770)
+  // window = tokens per chunk x whole chunks per inference window
+  // (src/audio_encoder.rs:807-810, src/audio_encoder_gpu.rs:883,1103)
+  g->wlen = feo((int)g->cs) * (c.n_window_infer / g->cs);
+  g->fdim = feo((int)c.n_mels);
+  const int64_t max_samples = (int64_t)(max_seconds * 16000.0);
+  g->max_chunks = (max_samples / 160 + g->cs - 1) / g->cs;
+  return QA_OK;
+}
+
 int load_aligner(const Checkpoint& ck, qa_ctx* ctx, int dtype, double max_seconds, int max_rows,
                  qah_aenc** enc_out, qah_tdec** dec_out, qah_aligner** al_out, std::string* err) {
   qah_ckpt_config c{};
   if (!ck.config(&c, err)) return QA_EINVAL;
   if (dtype != QA_F16 && dtype != QA_BF16) return *err = "dtype must be QA_F16 or QA_BF16", QA_EINVAL;
   if (max_seconds <= 0 || max_rows <= 0) return *err = "max_seconds and max_rows must be > 0", QA_EINVAL;
+  Geometry geo{};
+  if (int rc = tower_geometry(c, max_seconds, &geo, err)) return rc;
   // what this build's kernels and the aligner's fixed token ids cover
   if (c.d_model != c.enc_heads * 64)
     return *err = "audio tower heads must be 64 wide", QA_EUNSUPPORTED;
@@ -351,11 +377,9 @@ int load_aligner(const Checkpoint& ck, qa_ctx* ctx, int dtype, double max_second
   if (c.num_labels <= 0) return *err = "config.json gives no head width (id2label / classify_num)", QA_EINVAL;
   Loader L{ck, dtype, err};
   const std::string A = "thinker.audio_tower", T = "thinker.model";
-  const int cs = (int)(2 * c.n_window);
-  const int wlen = (int)(feo(cs) * c.n_window_infer / 100);
-  const int fdim = feo((int)c.n_mels);
+  const int cs = (int)geo.cs, wlen = (int)geo.wlen, fdim = (int)geo.fdim;
   const int64_t max_samples = (int64_t)(max_seconds * 16000.0);
-  const int max_chunks = (int)((max_samples / 160 + cs - 1) / cs);
+  const int max_chunks = (int)geo.max_chunks;
   const int64_t dm = c.d_model, cc = c.c_conv, ff = c.enc_ffn, hs = c.hidden, hd = c.hd;
 
   qah_aenc* enc = nullptr;
@@ -458,7 +482,10 @@ int load_aligner(const Checkpoint& ck, qa_ctx* ctx, int dtype, double max_second
   }
   {
     std::vector<float> cosv((size_t)max_rows * hd), sinv((size_t)max_rows * hd);
-    if (!L.call(qa_rope_tables(max_rows, (int)hd, c.rope_theta, cosv.data(), sinv.data()),
+    // theta 1e6 whatever config.json says: the aligner builds its tables with
+    // the constant (src/align_inference.rs:322-327); rope_theta only reaches
+    // the reference's other forwards.  Rounded to the run's format (:371-372).
+    if (!L.call(qa_rope_tables(max_rows, (int)hd, 1e6, (uint32_t)dtype, cosv.data(), sinv.data()),
                 "qa_rope_tables") ||
         !L.call(qah_tdec_set_rope(dec, cosv.data(), sinv.data(), max_rows), "qah_tdec_set_rope"))
       return cleanup(L.rc);
@@ -541,6 +568,20 @@ int qah_ckpt_load_aligner(qah_ckpt* c, qa_ctx* ctx, int dtype, double max_second
   const int rc = qah::load_aligner(*c->c, ctx, dtype, max_seconds, max_rows, enc, dec, al, &err);
   if (rc != QA_OK) qah::g_ckpt_err = err;
   return rc;
+}
+
+int qah_ckpt_geometry(qah_ckpt* c, double max_seconds, int64_t* out) {
+  if (!c || !out) return qah::g_ckpt_err = "qah_ckpt_geometry: null argument", QA_EINVAL;
+  std::string err;
+  qah_ckpt_config cfg{};
+  if (!c->c->config(&cfg, &err)) return qah::g_ckpt_err = err, QA_EINVAL;
+  qah::Geometry g{};
+  if (int rc = qah::tower_geometry(cfg, max_seconds, &g, &err)) return qah::g_ckpt_err = err, rc;
+  out[0] = g.cs;
+  out[1] = g.wlen;
+  out[2] = g.fdim;
+  out[3] = g.max_chunks;
+  return QA_OK;
 }
 
 void qah_ckpt_close(qah_ckpt* c) { delete c; }

@@ -60,6 +60,15 @@ class Checkpoint {
   std::string config_text_;
 };
 
+// The audio tower's geometry for config.json's fields: frames per chunk,
+// attention window in tokens, mel rows after the stem, chunks for
+// max_seconds of audio.  Refuses a geometry the tower or the decoder cannot
+// run (QA_EINVAL / QA_EUNSUPPORTED with a message in *err).
+struct Geometry {
+  int64_t cs, wlen, fdim, max_chunks;
+};
+int tower_geometry(const qah_ckpt_config& c, double max_seconds, Geometry* g, std::string* err);
+
 // The aligner (tower, decoder, head and embedding) built from a checkpoint:
 // shapes checked against config.json, weights narrowed to `dtype`.
 int load_aligner(const Checkpoint& ck, qa_ctx* ctx, int dtype, double max_seconds, int max_rows,

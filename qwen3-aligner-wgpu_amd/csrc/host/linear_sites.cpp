@@ -16,6 +16,7 @@
 #include <cstring>
 #include <thread>
 
+#include "../half_bits.h"
 #include "qa_host.h"
 #include "timing.hpp"
 
@@ -30,15 +31,9 @@ size_t elems_bytes(int64_t n) { return (size_t)n * 2; }
 int64_t align_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
 
 uint16_t narrow16(float v, int dtype) {
-  if (dtype == QA_BF16) {
-    uint32_t u;
-    memcpy(&u, &v, 4);
-    return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);  // src/shaders.rs:169-179
-  }
-  const _Float16 h = (_Float16)v;  // IEEE RNE
-  uint16_t b;
-  memcpy(&b, &h, 2);
-  return b;
+  // by integer arithmetic (half_bits.h): src/shaders.rs:169-179 for bf16,
+  // IEEE round to nearest even for f16
+  return dtype == QA_BF16 ? qa_half::bf16_from_f32(v) : qa_half::f16_from_f32(v);
 }
 
 uint64_t splitmix64(uint64_t x) {

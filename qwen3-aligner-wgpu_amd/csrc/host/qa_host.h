@@ -261,6 +261,14 @@ int qah_ckpt_read_config(qah_ckpt* c, qah_ckpt_config* out);
  * On success the caller owns all three (destroy the aligner first). */
 int qah_ckpt_load_aligner(qah_ckpt* c, qa_ctx* ctx, int dtype, double max_seconds, int max_rows,
                           qah_aenc** enc, qah_tdec** dec, qah_aligner** al);
+/* The tower geometry load_aligner uses for config.json and max_seconds:
+ * out[0] frames per chunk (2 n_window), out[1] the attention window in tokens
+ * (feo(cs) * (n_window_infer / cs), src/audio_encoder.rs:807-810), out[2] mel
+ * rows after the stem, out[3] chunks for max_seconds.  QA_EINVAL /
+ * QA_EUNSUPPORTED for a geometry the kernels cannot run (n_window,
+ * n_mels or n_window_infer not positive, a window shorter than a chunk,
+ * decoder heads not 128 wide, a GQA ratio above 2). */
+int qah_ckpt_geometry(qah_ckpt* c, double max_seconds, int64_t* out);
 void qah_ckpt_close(qah_ckpt* c);
 
 /* Time `iters` back-to-back launches of one descriptor (HIP events around the

@@ -16,6 +16,7 @@
 #include <string>
 #include <vector>
 
+#include "half_bits.h"
 #include "qa.h"
 #include "qa_internal.h"
 
@@ -165,6 +166,10 @@ qa::Plan plan_linear(const qa_linear_desc& d, int num_cus) {
   int forced_tile = -1, forced_splits = 0;
   if (const char* e = getenv("QA_TILE")) forced_tile = atoi(e);
   if (const char* e = getenv("QA_SPLITS")) forced_splits = atoi(e);
+  // A batch runs each problem as its own grid row (blockIdx.y) with no room
+  // for split-K partials, so batched calls are never split: the planner, not
+  // the shape, must not decide whether a valid batched call can run.
+  if (d.batch > 1) forced_splits = 1;
 
   int cands[qa::TILE_COUNT] = {qa::TILE_128x128, qa::TILE_256x128, qa::TILE_128x256,
                                qa::TILE_64x128,  qa::TILE_64x64,   qa::TILE_128x192,
@@ -750,16 +755,26 @@ int qa_log_mel(qa_ctx* ctx, const qa_mel_desc* d) {
   return e == hipSuccess ? ok() : hip_fail(e, "qa_log_mel launch");
 }
 
-int qa_rope_tables(int64_t positions, int hd, double theta, float* cos_out, float* sin_out) {
+// The run's 16-bit rounding of an f32 value, widened back to f32: IEEE RNE for
+// f16; (u + 0x7FFF + ((u >> 16) & 1)) >> 16 for bf16 (src/shaders.rs:169-179).
+float round16(float v, uint32_t dtype) {
+  if (dtype == QA_BF16) return qa_half::bf16_to_f32(qa_half::bf16_from_f32(v));
+  return qa_half::f16_to_f32(qa_half::f16_from_f32(v));
+}
+
+int qa_rope_tables(int64_t positions, int hd, double theta, uint32_t dtype, float* cos_out,
+                   float* sin_out) {
   if (positions <= 0 || hd <= 0 || hd % 2 || !(theta > 0.0) || !cos_out || !sin_out)
     return fail(QA_EINVAL, "qa_rope_tables: bad argument");
+  if (dtype != QA_F16 && dtype != QA_BF16)
+    return fail(QA_EINVAL, "qa_rope_tables: dtype %u is neither QA_F16 nor QA_BF16", dtype);
   const int half = hd / 2;
   std::vector<double> inv((size_t)half);
   for (int j = 0; j < half; ++j) inv[(size_t)j] = 1.0 / std::pow(theta, 2.0 * j / hd);
   for (int64_t p = 0; p < positions; ++p)
     for (int j = 0; j < half; ++j) {
       const double a = (double)p * inv[(size_t)j];
-      const float c = (float)std::cos(a), s = (float)std::sin(a);
+      const float c = round16((float)std::cos(a), dtype), s = round16((float)std::sin(a), dtype);
       cos_out[p * hd + j] = cos_out[p * hd + j + half] = c;
       sin_out[p * hd + j] = sin_out[p * hd + j + half] = s;
     }

@@ -110,6 +110,7 @@ def declare(L: ctypes.CDLL) -> None:
     L.qah_ckpt_read_f32.argtypes = [_vp, ctypes.c_char_p, _vp, ctypes.c_int64]
     L.qah_ckpt_read_config.argtypes = [_vp, ctypes.POINTER(CkptConfig)]
     L.qah_ckpt_load_aligner.argtypes = [_vp, _vp, _i, ctypes.c_double, _i] + [ctypes.POINTER(_vp)] * 3
+    L.qah_ckpt_geometry.argtypes = [_vp, ctypes.c_double, _vp]
     L.qah_ckpt_close.argtypes = [_vp]
     L.qah_ckpt_close.restype = None
     for name in ("qah_ckpt_open", "qah_ckpt_tensor", "qah_ckpt_read_h16", "qah_ckpt_read_f32",
@@ -192,23 +193,29 @@ class Checkpoint:
         _ck(host_lib().qah_ckpt_read_config(self.handle, ctypes.byref(c)))
         return {n: getattr(c, n) for n, _ in CkptConfig._fields_}
 
+    def geometry(self, max_seconds: float) -> dict:
+        """qah_ckpt_geometry: the tower geometry the loader uses."""
+        out = (ctypes.c_int64 * 4)()
+        _ck(host_lib().qah_ckpt_geometry(self.handle, max_seconds, out))
+        return dict(zip(("cs", "wlen", "fdim", "max_chunks"), list(out)))
+
     def load_aligner(self, ctx, dtype: int, max_seconds: float, max_rows: int):
         """(Aligner, AudioEncoder, TextDecoder) loaded from the checkpoint;
         close the aligner before the other two."""
         c = self.config()
+        geo = self.geometry(max_seconds)
         e, d, a = _vp(), _vp(), _vp()
         _ck(host_lib().qah_ckpt_load_aligner(self.handle, ctx.handle, dtype, max_seconds, max_rows,
                                              ctypes.byref(e), ctypes.byref(d), ctypes.byref(a)))
         f = lambda v: (v - 1) // 2 + 1  # noqa: E731
-        cs = 2 * c["n_window"]
-        max_samples = int(max_seconds * 16000)
+        cs = geo["cs"]
         enc = AudioEncoder.__new__(AudioEncoder)
         enc.ctx, enc.dtype, enc.layers = ctx, dtype, c["enc_layers"]
-        enc.max_chunks = (max_samples // 160 + cs - 1) // cs
+        enc.max_chunks = geo["max_chunks"]
         enc.n_mels, enc.cs, enc.c_conv, enc.d_model = c["n_mels"], cs, c["c_conv"], c["d_model"]
         enc.nh, enc.ffn, enc.out_dim = c["enc_heads"], c["enc_ffn"], c["out_dim"]
-        enc.wlen = f(f(f(cs))) * c["n_window_infer"] // 100
-        enc.h3, enc.w3 = f(f(f(c["n_mels"]))), f(f(f(cs)))
+        enc.wlen = geo["wlen"]
+        enc.h3, enc.w3 = geo["fdim"], f(f(f(cs)))
         enc.handle = e.value
         dec = TextDecoder.__new__(TextDecoder)
         dec.ctx, dec.dtype, dec.layers, dec.max_rows = ctx, dtype, c["layers"], max_rows

@@ -126,7 +126,7 @@ def build_aligner(pkg, ctx, dtype: int, w: dict, max_seconds: float, max_rows: i
         for li, l in enumerate(w["dec"]):
             dec.load_layer(li, l["q"], l["k"], l["v"], l["o"], l["gate"], l["up"], l["down"],
                            l["iln"], l["pln"], l["qn"], l["kn"])
-        dec.set_rope(*pkg.rope_tables(max_rows, T["hd"], 1e6))
+        dec.set_rope(*pkg.rope_tables(max_rows, T["hd"], 1e6, dtype))
         al = host.Aligner(ctx, enc, dec, VOCAB, LABELS, SEGMENT_MS, max_samples)
     except Exception:
         enc.close()

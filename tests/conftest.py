@@ -279,13 +279,27 @@ def _assert_within(got_bits, want_bits, bound, orc, dtype, s):
     return s
 
 
-def rope_tables(rows, hd, pos0, theta=1e6):
+def round16(x, dtype):
+    """f32 values rounded to the 16-bit format and widened back: numpy's IEEE
+    cast for f16; (u + 0x7FFF + ((u >> 16) & 1)) >> 16 for bf16
+    (src/shaders.rs:169-179)."""
+    x = np.asarray(x, np.float32)
+    if dtype == 0:
+        return x.astype(np.float16).astype(np.float32)
+    u = x.view(np.uint32).astype(np.uint64)
+    return (((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16).astype(np.uint32).view(np.float32)
+
+
+def rope_tables(rows, hd, pos0, theta=1e6, dtype=0):
     """cos/sin [pos][hd] as src/mrope.rs:55-82 builds them for text positions:
-    angle(pos, j) = pos * theta^(-2j/hd), the second half repeating the first."""
+    angle(pos, j) = pos * theta^(-2j/hd) in f64, the second half repeating the
+    first, rounded to f32 and then to the run's 16-bit format, as the reference
+    narrows both tables before the decoder reads them
+    (src/align_inference.rs:371-372,394-395; src/cpu_decoder.rs:247)."""
     half = hd // 2
     inv = 1.0 / theta ** (2.0 * np.arange(half) / hd)
     pos = np.arange(pos0 + rows, dtype=np.float64)[:, None]
     ang = pos * inv[None, :]
     c = np.concatenate([np.cos(ang), np.cos(ang)], axis=1).astype(np.float32)
     s = np.concatenate([np.sin(ang), np.sin(ang)], axis=1).astype(np.float32)
-    return c, s
+    return round16(c, dtype), round16(s, dtype)

@@ -203,6 +203,14 @@ def test_rope_tables_match_the_text_position_definition(pkg):
     with repeated halves (src/mrope.rs:55-89 for text positions)."""
     import numpy as np
     from conftest import rope_tables
-    c, s = pkg.rope_tables(300, 128, 1e6)
-    wc, ws = rope_tables(300, 128, 0, theta=1e6)
-    assert np.array_equal(c, wc) and np.array_equal(s, ws)
+    for dt in (pkg.F16, pkg.BF16):
+        c, s = pkg.rope_tables(300, 128, 1e6, dt)
+        wc, ws = rope_tables(300, 128, 0, theta=1e6, dtype=dt)
+        assert np.array_equal(c, wc) and np.array_equal(s, ws)
+    # every value is a 16-bit value widened: the reference narrows both tables
+    # (src/align_inference.rs:371-372, 394-395)
+    c, s = pkg.rope_tables(300, 128, 1e6, pkg.F16)
+    assert np.array_equal(c, c.astype(np.float16).astype(np.float32))
+    c, s = pkg.rope_tables(300, 128, 1e6, pkg.BF16)
+    assert not (c.view(np.uint32) & 0xFFFF).any() and not (s.view(np.uint32) & 0xFFFF).any()
+    assert pkg.lib().qa_rope_tables(4, 128, 1e6, 7, c.ctypes.data, s.ctypes.data) == pkg.QA_EINVAL

@@ -167,3 +167,48 @@ def test_errors(tmp_path, host):
             ck.read_f32("i")
         with pytest.raises(host.CheckpointError, match="config.json missing"):
             ck.config()
+
+
+def _geometry_dir(tmp_path, hf=False, **audio_text):
+    dims = dict(d_model=128, enc_layers=1, ffn=256, c_conv=64, hidden=256, vocab=151936,
+                inter=384, layers=1, nqh=2, nkvh=1, hd=128, labels=7)
+    cfg = aligner_config(dims, hf)
+    a = cfg["audio_config"] if hf else cfg["thinker_config"]["audio_config"]
+    t = cfg["text_config"] if hf else cfg["thinker_config"]["text_config"]
+    for k, v in audio_text.items():
+        (a if k in a else t)[k] = v
+    write_checkpoint(str(tmp_path), {"x": np.zeros(1, np.float32)}, cfg, hf=hf)
+    return str(tmp_path)
+
+
+@pytest.mark.parametrize("n_window,n_window_infer,wlen", [(50, 800, 104), (50, 250, 26),
+                                                          (30, 400, 48), (40, 250, 30)])
+def test_loader_window_geometry(tmp_path, host, n_window, n_window_infer, wlen):
+    """The tower's attention window is feo(cs) * (n_window_infer / cs) tokens
+    with cs = 2 n_window and an integer division by cs
+    (src/audio_encoder.rs:807-810, src/audio_encoder_gpu.rs:883,1103): not
+    feo(cs) * n_window_infer / 100, which agrees only at cs = 100."""
+    d = _geometry_dir(tmp_path, n_window=n_window, n_window_infer=n_window_infer)
+    f = lambda v: (v - 1) // 2 + 1  # noqa: E731
+    cs = 2 * n_window
+    assert f(f(f(cs))) * (n_window_infer // cs) == wlen
+    with host.Checkpoint(d) as ck:
+        g = ck.geometry(10.0)
+    assert g == dict(cs=cs, wlen=wlen, fdim=16, max_chunks=(10 * 16000 // 160 + cs - 1) // cs)
+
+
+@pytest.mark.parametrize("field,value,code", [("n_window", 0, -1), ("num_mel_bins", 0, -1),
+                                              ("n_window_infer", 60, -1), ("head_dim", 64, -4),
+                                              ("num_key_value_heads", 3, -1),
+                                              ("num_attention_heads", 8, -4)],
+                         ids=["n_window-0", "n_mels-0", "window-below-chunk", "hd-64",
+                              "heads-not-multiple", "gqa-4"])
+def test_loader_refuses_unsupported_geometry(tmp_path, host, field, value, code):
+    """A geometry the kernels cannot run is refused up front with QA_EINVAL
+    (-1) or QA_EUNSUPPORTED (-4) and a message, before anything is sized or
+    allocated (n_window = 0 would otherwise divide by zero)."""
+    d = _geometry_dir(tmp_path, **{field: value})
+    with host.Checkpoint(d) as ck:
+        with pytest.raises(host.CheckpointError) as e:
+            ck.geometry(10.0)
+        assert e.value.code == code and e.value.message

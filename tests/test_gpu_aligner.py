@@ -23,9 +23,16 @@ Gates:
     GPU path); the repaired times equal the oracle's repair of the GPU's
     classes;
   * at the benchmark's end-to-end config (300 s, 120 words, 18 + 28 layers)
-    the classes against the committed oracle fixture
-    (tests/golden/e2e_300s.json, written by tests/golden/make_e2e_golden.py
-    on the same seeded inputs), with the same near-tie rule.
+    against the committed oracle fixture (tests/golden/e2e_300s.json / .npz,
+    written by tests/golden/make_e2e_golden.py on the same seeded inputs):
+    the final hidden rows at the 240 <timestamp> slots and the logits at each
+    slot's 8 best labels (the gates of tests/chains.py, which
+    tests/test_e2e_gate.py shows reject planted mistakes), the classes with
+    the same near-tie rule, and the distance to the reference CPU path's
+    forward (its f32 tower).  With random-init weights the <timestamp>
+    embedding dominates those rows, so every slot picks the same class: the
+    classes alone would not tell a correct forward from a wrong one, the rows
+    and logits do.
 """
 from __future__ import annotations
 
@@ -72,6 +79,7 @@ def _clear(gap, rms):
     return np.asarray(gap) > NEAR_TIE * np.asarray(rms)
 
 
+
 @pytest.mark.parametrize("dtype,seconds,n_words,layers", [(F16, 7.37, 16, (2, 3)),
                                                           (BF16, 4.0, 9, (1, 2))],
                          ids=["f16-7s", "bf16-4s"])
@@ -81,7 +89,7 @@ def test_aligner_against_oracle_chain(ctx, pkg, orc, dtype, seconds, n_words, la
     x, words = _inputs(seconds, n_words, 11)
     g = _run(pkg, ctx, dtype, w, x, words, 512)
     r = oracle_aligner(orc, dtype, w, x, words, pkg.mel_filterbank(),
-                       lambda n: pkg.rope_tables(n, 128, 1e6))
+                       lambda n: pkg.rope_tables(n, 128, 1e6, dtype))
     # the assembled input
     assert g["info"]["n_audio"] == r["n_audio"] and g["info"]["seq"] == r["ids"].size
     ids, src, ts = assemble(r["n_audio"], words)
@@ -112,10 +120,22 @@ def test_aligner_against_oracle_chain(ctx, pkg, orc, dtype, seconds, n_words, la
     assert list(g["fixed"]) == orc.fix_timestamps(list(g["raw"]))
 
 
-def test_aligner_e2e_300s_against_fixture(ctx, pkg):
+def test_aligner_e2e_300s_against_fixture(ctx, pkg, orc):
+    """BASELINE config 5 against the oracle's forward of the same seeded
+    inputs (tests/golden/e2e_300s.json / .npz):
+      * the final hidden rows at the 240 <timestamp> slots against the 16-bit
+        chain's (rows_gate: MAE and one ulp of relative RMS);
+      * the logits at each slot's 8 best labels within what the two sets of
+        rows allow (logits_gate);
+      * the classes identical at every slot with a clear oracle margin;
+      * against the reference CPU path's forward (f32 tower, cpu_ref): the
+        rows by the north star's MAE, the classes identical at clear slots,
+        the relative RMS reported."""
     from qwen3_aligner_wgpu_amd import synthetic as syn
-    path = os.path.join(HERE, "golden", "e2e_300s.json")
-    gold = json.load(open(path))
+    from chains import logits_gate, rows_gate
+    path = os.path.join(HERE, "golden", "e2e_300s")
+    gold = json.load(open(path + ".json"))
+    arr = np.load(path + ".npz")
     c = gold["config"]
     w = syn.aligner_weights(c["dtype"], c["enc_layers"], c["dec_layers"], c["seed"])
     x = syn.synthetic_audio(c["seconds"], c["seed"])
@@ -127,9 +147,55 @@ def test_aligner_e2e_300s_against_fixture(ctx, pkg):
     g = _run(pkg, ctx, c["dtype"], w, x, words, 4352)
     assert g["info"]["seq"] == gold["seq"] and g["info"]["n_audio"] == gold["n_audio"]
     assert dg(g["ids"]) == gold["digests"]["ids"]
+    assert list(g["ts"]) == gold["ts"]
+    rows = g["h"][g["ts"]]
+    ok, st = rows_gate(orc, c["dtype"], rows, arr["chain16_rows"])
+    ok_lg, use = logits_gate(orc, c["dtype"], rows, g["logits"], arr["chain16_rows"],
+                             arr["chain16_top_idx"], arr["chain16_top_logits"], w["norm_w"],
+                             w["score"])
     want = np.array(gold["classes"])
     clear = _clear(gold["gap"], gold["logit_rms"])
     same = g["classes"] == want
-    print(f"e2e 300 s: classes identical at {same.sum()}/{want.size} slots, "
-          f"{clear.sum()} with a clear oracle margin; samples bit-identical: {same_audio}")
+    print(f"e2e 300 s vs the 16-bit chain: rows {st}; logits bound use {use:.3f}; classes "
+          f"identical at {same.sum()}/{want.size} slots, {clear.sum()} with a clear margin; "
+          f"samples bit-identical: {same_audio}")
+    assert ok, st
+    assert ok_lg, use
     assert same[clear].all(), np.nonzero(~same & clear)
+    # the reference CPU path (f32 tower)
+    ref = gold["cpu_ref"]
+    _, st_ref = rows_gate(orc, c["dtype"], rows, arr["cpu_ref_rows"])
+    want_ref = np.array(ref["classes_f32_head"])
+    clear_ref = _clear(ref["gap"], ref["logit_rms"])
+    same_ref = g["classes"] == want_ref
+    print(f"e2e 300 s vs the reference CPU path (f32 tower): rows {st_ref}; classes identical at "
+          f"{same_ref.sum()}/{want_ref.size} slots ({clear_ref.sum()} clear)")
+    assert st_ref["mae"] <= 1e-3, st_ref
+    assert same_ref[clear_ref].all(), np.nonzero(~same_ref & clear_ref)
+
+
+def test_failed_prepare_forgets_the_previous_clip(ctx, pkg):
+    """A prepare that fails (here: an audio placeholder id among the words)
+    leaves nothing prepared: forward() refuses with QA_EINVAL instead of
+    aligning the previous clip, and the host arrays describe nothing."""
+    from qwen3_aligner_wgpu_amd import synthetic as syn
+    w = syn.aligner_weights(F16, 1, 1, seed=3)
+    x, words = _inputs(2.0, 3, 4)
+    al, enc, dec = syn.build_aligner(pkg, ctx, F16, w, 2.1, 256)
+    try:
+        al.prepare(x, words)
+        al.forward()
+        with pytest.raises(pkg.QAError) as e:
+            al.prepare(x, words + [[151676]])  # audio_pad among the word ids
+        assert e.value.code == pkg.QA_EINVAL
+        with pytest.raises(pkg.QAError) as e:
+            al.forward()
+        assert e.value.code == pkg.QA_EINVAL
+        # a good prepare afterwards works again
+        al.prepare(x, words)
+        al.forward()
+        assert al.result()[0].size == 2 * len(words)
+    finally:
+        al.close()
+        enc.close()
+        dec.close()

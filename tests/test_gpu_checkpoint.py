@@ -131,7 +131,7 @@ def _direct(pkg, ctx, t, store, max_seconds, max_rows):
             "mlp.gate_proj", "mlp.up_proj", "mlp.down_proj")],
             *[n16(f"{p}.{n}.weight") for n in ("input_layernorm", "post_attention_layernorm",
                                                "self_attn.q_norm", "self_attn.k_norm")])
-    dec.set_rope(*pkg.rope_tables(max_rows, D["hd"], 1e6))
+    dec.set_rope(*pkg.rope_tables(max_rows, D["hd"], 1e6, F16))
     al = host.Aligner(ctx, enc, dec, D["vocab"], D["labels"], 80.0, max_samples)
     al.load_embed(h16(f"{T}.embed_tokens.weight"))
     al.load_head(v[f"{T}.norm.weight"], v["score.weight"])

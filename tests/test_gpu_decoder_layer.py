@@ -80,7 +80,7 @@ def test_decoder_layer_per_stage(ctx, pkg, orc, dtype, rows, attn_flags):
     ws = _weights(rng, orc, dtype, 1)
     w = ws[0]
     h0 = orc.h16_from_f32(rng.standard_normal((rows, HID)).astype(np.float32), dtype)
-    cos, sin = rope_tables(rows, HD, 0)
+    cos, sin = rope_tables(rows, HD, 0, dtype=dtype)
     g, cap = _run_gpu(ctx, dtype, ws, h0, cos, sin, attn_flags,
                       ("normed", "qkv", "q", "k_cache", "v_cache", "attn", "norm2", "act", "h"))
     # 1. input RMSNorm
@@ -130,7 +130,7 @@ def test_decoder_two_layers_chain(ctx, pkg, orc, dtype, rows):
     rng = np.random.default_rng(7 * rows + dtype)
     ws = _weights(rng, orc, dtype, 2)
     h0 = orc.h16_from_f32(rng.standard_normal((rows, HID)).astype(np.float32), dtype)
-    cos, sin = rope_tables(rows, HD, 0)
+    cos, sin = rope_tables(rows, HD, 0, dtype=dtype)
     g, cap = _run_gpu(ctx, dtype, ws, h0, cos, sin, 0, ("h",))
     h = h0
     for w in ws:

@@ -79,7 +79,7 @@ def _rope_case(ctx, pkg, orc, dtype, rows, nqh, nkvh, hd, pos0, start, cap, seed
     qkv = _h16(orc, 2.0 * rng.standard_normal((rows, ld)), dtype)
     qn = (1.0 + 0.2 * rng.standard_normal(hd)).astype(np.float32)
     kn = (1.0 + 0.2 * rng.standard_normal(hd)).astype(np.float32)
-    c, s = rope_tables(rows, hd, pos0)
+    c, s = rope_tables(rows, hd, pos0, dtype=dtype)
     kc0 = np.full((nkvh, cap, hd), 0x1234, np.uint16)
     vc0 = np.full((nkvh, hd, cap), 0x4321, np.uint16)
     bufs = [ctx.to_device(a) for a in (qkv, qn, kn, c, s, kc0, vc0)]

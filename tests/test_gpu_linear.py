@@ -154,57 +154,97 @@ def test_batched(ctx, pkg, orc, dtype):
     assert_parity(got.reshape(batch, m, n), want, orc, dtype, ulp_tol=1)
 
 
+@pytest.mark.parametrize("dtype", [0, 1], ids=["f16", "bf16"])
+def test_batched_long_k_is_never_split(ctx, pkg, orc, dtype):
+    """A batched call whose shape alone would make the planner split K (few
+    tiles, long K) runs unsplit instead of failing with QA_EUNSUPPORTED: the
+    planner, not the caller's valid shape, decides the split."""
+    rng = np.random.default_rng(19)
+    batch, m, n, k = 3, 64, 128, 4096
+    a = _h16(orc, rng.standard_normal((batch, m, k)), dtype)
+    w = _h16(orc, 0.02 * rng.standard_normal((batch, n, k)), dtype)
+    c0 = np.zeros((batch, m, n), np.uint16)
+    got = _run(ctx, pkg, dtype, a.reshape(batch * m, k), w.reshape(batch * n, k),
+               c0.reshape(batch * m, n), m=m, n=n, k=k, batch=batch, bsa=m * k, bsb=n * k,
+               bsc=m * n)
+    want = orc.linear(dtype, a, w, c0.copy(), flags=orc.EXACT, m=m, n=n, k=k, batch=batch,
+                      bsa=m * k, bsb=n * k, bsc=m * n)
+    assert_parity(got.reshape(batch, m, n), want, orc, dtype, ulp_tol=1)
+    # a split forced through the environment is not applied to a batched call either
+    os.environ["QA_SPLITS"] = "4"
+    try:
+        got2 = _run(ctx, pkg, dtype, a.reshape(batch * m, k), w.reshape(batch * n, k),
+                    c0.reshape(batch * m, n), m=m, n=n, k=k, batch=batch, bsa=m * k,
+                    bsb=n * k, bsc=m * n)
+    finally:
+        del os.environ["QA_SPLITS"]
+    assert np.array_equal(got2, got)
+
+
+@pytest.mark.parametrize("dtype", [0, 1], ids=["f16", "bf16"])
 @pytest.mark.parametrize("tile", [0, 1, 2, 3, 4, 5, 6])
 @pytest.mark.parametrize("splits", [1, 2, 3, 5])
-def test_forced_tiles_and_splits(ctx, pkg, orc, tile, splits):
-    """Every tile shape, with and without split-K (incl. uneven k ranges)."""
-    rng = np.random.default_rng(tile * 10 + splits)
+def test_forced_tiles_and_splits(ctx, pkg, orc, tile, splits, dtype):
+    """Every tile shape, with and without split-K (incl. uneven k ranges), in
+    both formats: bias + residual, bias + GELU, and SiLU.up."""
+    rng = np.random.default_rng(tile * 10 + splits + 100 * dtype)
     m, n, k = 300, 512, 1216
-    a, w = _case(rng, orc, 0, m, n, k)
-    c0 = _h16(orc, rng.standard_normal((m, n)), 0)
-    bias = _h16(orc, 0.1 * rng.standard_normal(n), 0)
+    a, w = _case(rng, orc, dtype, m, n, k)
+    c0 = _h16(orc, rng.standard_normal((m, n)), dtype)
+    bias = _h16(orc, 0.1 * rng.standard_normal(n), dtype)
     os.environ["QA_TILE"], os.environ["QA_SPLITS"] = str(tile), str(splits)
     try:
-        got = _run(ctx, pkg, 0, a, w, c0, flags=pkg.ACCUMULATE, bias=bias)
-        again = _run(ctx, pkg, 0, a, w, c0, flags=pkg.ACCUMULATE, bias=bias)
-        gu_w = _h16(orc, 0.05 * rng.standard_normal((2 * 256, k)), 0)
-        act = _run(ctx, pkg, 0, a, gu_w, np.zeros((m, 256), np.uint16), flags=pkg.EPI_SILU_MUL)
+        got = _run(ctx, pkg, dtype, a, w, c0, flags=pkg.ACCUMULATE, bias=bias)
+        again = _run(ctx, pkg, dtype, a, w, c0, flags=pkg.ACCUMULATE, bias=bias)
+        gelu = _run(ctx, pkg, dtype, a, w, np.zeros_like(c0), flags=pkg.EPI_GELU, bias=bias)
+        gu_w = _h16(orc, 0.05 * rng.standard_normal((2 * 256, k)), dtype)
+        act = _run(ctx, pkg, dtype, a, gu_w, np.zeros((m, 256), np.uint16), flags=pkg.EPI_SILU_MUL)
     finally:
         del os.environ["QA_TILE"], os.environ["QA_SPLITS"]
-    exact = orc.linear(0, a, w, c0.copy(), flags=orc.ACCUMULATE | orc.EXACT, bias=bias)
-    assert_parity(got, exact, orc, 0, ulp_tol=1)
+    exact = orc.linear(dtype, a, w, c0.copy(), flags=orc.ACCUMULATE | orc.EXACT, bias=bias)
+    assert_parity(got, exact, orc, dtype, ulp_tol=1)
     assert np.array_equal(got, again), "split-K reduction must be deterministic"
-    act_exact = orc.linear(0, a, gu_w, np.zeros((m, 256), np.uint16),
+    gelu_exact = orc.linear(dtype, a, w, np.zeros_like(c0), flags=orc.EPI_GELU | orc.EXACT,
+                            bias=bias)
+    assert_parity(gelu, gelu_exact, orc, dtype, ulp_tol=1)
+    act_exact = orc.linear(dtype, a, gu_w, np.zeros((m, 256), np.uint16),
                            flags=orc.EPI_SILU_MUL | orc.EXACT)
-    gu_exact = orc.linear(0, a, gu_w, np.zeros((m, 512), np.uint16), flags=orc.EXACT)
-    assert_silu_mul(act, act_exact, a, gu_w, gu_exact, orc, 0, k)
+    gu_exact = orc.linear(dtype, a, gu_w, np.zeros((m, 512), np.uint16), flags=orc.EXACT)
+    assert_silu_mul(act, act_exact, a, gu_w, gu_exact, orc, dtype, k, rel_tol=SILU_REL[dtype])
 
 
+@pytest.mark.parametrize("dtype", [0, 1], ids=["f16", "bf16"])
 @pytest.mark.parametrize("group_m", [1, 3, 5, 8, 1000])
 @pytest.mark.parametrize("tile,splits", [(4, 1), (0, 1), (3, 2), (5, 1), (6, 1)])
-def test_tile_enumeration_bands(ctx, pkg, orc, group_m, tile, splits):
+def test_tile_enumeration_bands(ctx, pkg, orc, group_m, tile, splits, dtype):
     """Every band height of the tile enumeration (including ones that do not
     divide the tile grid, and more than its height) maps blocks onto tiles
     one to one: C starts as noise and must end equal to the exactly rounded
-    result everywhere (a tile computed twice leaves another one untouched)."""
-    rng = np.random.default_rng(40 + group_m + 10 * tile)
+    result everywhere (a tile computed twice leaves another one untouched).
+    Plain, bias + GELU and SiLU.up epilogues, both formats."""
+    rng = np.random.default_rng(40 + group_m + 10 * tile + 1000 * dtype)
     m, n, k = 600, 1472, 640   # ragged in m and n for every tile shape
-    a, w = _case(rng, orc, 0, m, n, k)
-    c0 = _h16(orc, rng.standard_normal((m, n)), 0)
+    a, w = _case(rng, orc, dtype, m, n, k)
+    c0 = _h16(orc, rng.standard_normal((m, n)), dtype)
+    bias = _h16(orc, 0.1 * rng.standard_normal(n), dtype)
     os.environ.update(QA_TILE=str(tile), QA_SPLITS=str(splits), QA_GROUP_M=str(group_m))
     try:
-        got = _run(ctx, pkg, 0, a, w, c0)
-        gu_w = _h16(orc, 0.05 * rng.standard_normal((2 * 736, k)), 0)
-        act = _run(ctx, pkg, 0, a, gu_w, np.zeros((m, 736), np.uint16), flags=pkg.EPI_SILU_MUL)
+        got = _run(ctx, pkg, dtype, a, w, c0)
+        gelu = _run(ctx, pkg, dtype, a, w, c0, flags=pkg.EPI_GELU, bias=bias)
+        gu_w = _h16(orc, 0.05 * rng.standard_normal((2 * 736, k)), dtype)
+        act = _run(ctx, pkg, dtype, a, gu_w, np.zeros((m, 736), np.uint16), flags=pkg.EPI_SILU_MUL)
     finally:
         for key in ("QA_TILE", "QA_SPLITS", "QA_GROUP_M"):
             del os.environ[key]
-    exact = orc.linear(0, a, w, np.zeros_like(c0), flags=orc.EXACT)
-    assert_parity(got, exact, orc, 0, ulp_tol=1)
-    act_exact = orc.linear(0, a, gu_w, np.zeros((m, 736), np.uint16),
+    exact = orc.linear(dtype, a, w, np.zeros_like(c0), flags=orc.EXACT)
+    assert_parity(got, exact, orc, dtype, ulp_tol=1)
+    gelu_exact = orc.linear(dtype, a, w, np.zeros_like(c0), flags=orc.EPI_GELU | orc.EXACT,
+                            bias=bias)
+    assert_parity(gelu, gelu_exact, orc, dtype, ulp_tol=1)
+    act_exact = orc.linear(dtype, a, gu_w, np.zeros((m, 736), np.uint16),
                            flags=orc.EPI_SILU_MUL | orc.EXACT)
-    gu_exact = orc.linear(0, a, gu_w, np.zeros((m, 1472), np.uint16), flags=orc.EXACT)
-    assert_silu_mul(act, act_exact, a, gu_w, gu_exact, orc, 0, k)
+    gu_exact = orc.linear(dtype, a, gu_w, np.zeros((m, 1472), np.uint16), flags=orc.EXACT)
+    assert_silu_mul(act, act_exact, a, gu_w, gu_exact, orc, dtype, k, rel_tol=SILU_REL[dtype])
 
 
 @pytest.mark.parametrize("dtype", [0, 1], ids=["f16", "bf16"])

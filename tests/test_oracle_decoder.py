@@ -75,7 +75,7 @@ def _qkv_case(orc, dtype, rows, nqh, nkvh, hd, seed):
 def test_qk_norm_rope_closed_form_and_layouts(orc, dtype):
     rows, nqh, nkvh, hd, pos0, start, cap, eps = 23, 4, 2, 128, 40, 40, 96, 1e-6
     qkv, qn, kn = _qkv_case(orc, dtype, rows, nqh, nkvh, hd, 2)
-    c, s = rope_tables(rows, hd, pos0)
+    c, s = rope_tables(rows, hd, pos0, dtype=dtype)
     kc = np.full((nkvh, cap, hd), 0x1234, np.uint16)
     vc = np.full((nkvh, hd, cap), 0x4321, np.uint16)
     q = orc.qk_norm_rope(dtype, qkv, nqh, nkvh, hd, qn, kn, c, s, pos0, eps, kc, vc, start)
