@@ -166,6 +166,145 @@ def bench_decoder(pkg, host, ctx, m, warmup, steps, tdec=None):
     return dec, ev_ms, wall_ms, sites
 
 
+# ---- per-launch timing protocol: >= 200 back-to-back launches after 20
+# warm-ups, median and p10 / p90 of the per-launch durations; "warm" repeats
+# one weight matrix (L2 / MALL resident), "cold" cycles through copies that
+# together exceed the 256 MB MALL, so every launch fetches its W from HBM ----
+
+def dist(ms):
+    """Per-launch ms -> {median, p10, p90} in microseconds."""
+    us = np.asarray(ms, np.float64) * 1e3
+    return {"median": round(float(np.median(us)), 2), "p10": round(float(np.percentile(us, 10)), 2),
+            "p90": round(float(np.percentile(us, 90)), 2), "launches": int(us.size)}
+
+
+# site -> (n rows of W, k, flags name, output columns); fused as the reference
+# runs them (src/decoder.rs:1321-1657) and unfused as its CPU path does
+# (q, k, v and gate, up separately, src/cpu_decoder.rs:416-512)
+def dec_sites(unfused):
+    h, q, kv, it = DEC["hidden"], DEC["q_dim"], DEC["kv_dim"], DEC["inter"]
+    if unfused:
+        return {"q": (q, h, 0), "k": (kv, h, 0), "v": (kv, h, 0), "o": (h, q, 1),
+                "gate": (it, h, 0), "up": (it, h, 0), "down": (h, it, 1)}
+    return {"qkv": (q + 2 * kv, h, 0), "o": (h, q, 1), "gu": (2 * it, h, 2), "down": (h, it, 1)}
+
+
+class SiteSet:
+    """Device copies of every decoder layer's weights for the per-site
+    protocol (fused or unfused layout) plus the fixed activations, and one
+    qa_linear descriptor per (site, layer)."""
+
+    def __init__(self, pkg, host, ctx, m, layers, unfused):
+        self.pkg, self.ctx, self.m, self.unfused = pkg, ctx, m, unfused
+        self.sites = dec_sites(unfused)
+        self.bufs = []
+        h, q, it = DEC["hidden"], DEC["q_dim"], DEC["inter"]
+        put = lambda a: self._keep(ctx.to_device(a))  # noqa: E731
+        self.x = {"h": put(rmsnormed(host, 0, 1, (m, h), 0)), "q": put(rmsnormed(host, 0, 2, (m, q), 0)),
+                  "it": put(host.synth_normal(0, 5, (m, it), 0, 0.5))}
+        self.out = {"wide": self._keep(ctx.alloc(m * 2 * it * 2)),
+                    "res": put(host.synth_normal(0, 4, (m, h)))}
+        self.descs = {s: [] for s in self.sites}
+        for li in range(layers):
+            w = decoder_weights(host, li)
+            mats = dict(q=w["q"], k=w["k"], v=w["v"], o=w["o"], gate=w["gate"], up=w["up"],
+                        down=w["down"]) if unfused else dict(
+                qkv=np.concatenate([w["q"], w["k"], w["v"]]), o=w["o"],
+                gu=np.concatenate([w["gate"], w["up"]]), down=w["down"])
+            for s, (n, k, fl) in self.sites.items():
+                dw = put(np.ascontiguousarray(mats[s]))
+                a = self.x["q"] if k == q else self.x["it"] if k == it else self.x["h"]
+                if fl == 1:
+                    d = pkg.linear_desc(pkg.F16, m, n, k, a, dw, self.out["res"], flags=pkg.ACCUMULATE)
+                elif fl == 2:
+                    d = pkg.linear_desc(pkg.F16, m, n, k, a, dw, self.out["wide"], flags=pkg.EPI_SILU_MUL)
+                else:
+                    d = pkg.linear_desc(pkg.F16, m, n, k, a, dw, self.out["wide"])
+                self.descs[s].append(d)
+
+    def _keep(self, b):
+        self.bufs.append(b)
+        return b
+
+    def flops(self, site):
+        n, k, fl = self.sites[site]
+        return 2 * self.m * n * k
+
+    def close(self):
+        for b in self.bufs:
+            b.free()
+        self.bufs = []
+
+
+def site_protocol(host, ctx, ss, warm_iters=200, cold_iters=280):
+    """Per site: cold (cycling through every layer's W, 880 MB fused) and warm
+    (layer 0's W repeated) per-launch distributions; and one back-to-back pass
+    over the layers' sites in the reference's order, ms per 28-layer step."""
+    out = {}
+    for s, descs in ss.descs.items():
+        cold = dist(host.time_linears_each(ss.ctx, descs, 20, cold_iters))
+        warm = dist(host.time_linears_each(ss.ctx, descs[:1], 20, warm_iters))
+        out[s] = {"cold": cold, "warm": warm,
+                  "tflops_cold_median": round(ss.flops(s) / (cold["median"] * 1e-6) / 1e12, 1)}
+    seq = [ss.descs[s][li] for li in range(DEC["layers"]) for s in ss.sites]
+    ms = host.time_linears_each(ss.ctx, seq, 20, 2 * len(seq))
+    step_ms = float(ms.sum()) / 2
+    flops = sum(ss.flops(s) for s in ss.sites) * DEC["layers"]
+    return out, {"step_ms_back_to_back": round(step_ms, 4),
+                 "tflops": round(flops / (step_ms * 1e-3) / 1e12, 1),
+                 "note": "eager launches, no graph: each site's GEMM in layer order over 28 "
+                         "layers, ms summed over per-launch events"}
+
+
+def config1_protocol(pkg, host, ctx):
+    """Config 1 (x [256,1024] . W[3072,1024]^T, HBM-bound): warm (one W) and
+    cold (48 copies of W, 302 MB > the 256 MB MALL), with the algorithmic
+    bytes over the median launch."""
+    m, n, k = 256, 3072, 1024
+    a = ctx.to_device(host.synth_normal(0, 11, (m, k)))
+    c = ctx.alloc(m * n * 2)
+    ws = [ctx.to_device(host.synth_normal(0, 12 if i == 0 else 1200 + i, (n, k), 0, 0.02))
+          for i in range(48)]
+    descs = [pkg.linear_desc(pkg.F16, m, n, k, a, w, c) for w in ws]
+    warm = dist(host.time_linears_each(ctx, descs[:1], 20, 200))
+    cold = dist(host.time_linears_each(ctx, descs, 20, 288))
+    algo = 2 * (m * k + n * k + m * n)
+    for b in [a, c] + ws:
+        b.free()
+    f = 2 * m * n * k
+    return {"warm": warm, "cold": cold, "algorithmic_bytes": algo,
+            "hbm_gbs_cold_median": round(algo / (cold["median"] * 1e-6) / 1e9, 1),
+            "hbm_frac_cold_median": round(algo / (cold["median"] * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
+            "tflops_cold_median": round(f / (cold["median"] * 1e-6) / 1e12, 1),
+            "tflops_warm_median": round(f / (warm["median"] * 1e-6) / 1e12, 1)}
+
+
+def config2_protocol(pkg, host, ctx):
+    """Config 2 (the MLP block at M = 512: gate|up + SiLU.up, then down +
+    residual): per-launch distributions of the pair, warm and cold (16 weight
+    sets, 320 MB)."""
+    m, hid, it = 512, 1024, 3072
+    x = ctx.to_device(host.synth_normal(0, 21, (m, hid)))
+    act = ctx.alloc(m * it * 2)
+    sets = [(ctx.to_device(host.synth_normal(0, 22 if i == 0 else 2200 + 2 * i, (2 * it, hid), 0, 0.02)),
+             ctx.to_device(host.synth_normal(0, 23 if i == 0 else 2201 + 2 * i, (hid, it), 0, 0.02)))
+            for i in range(16)]
+    descs = []
+    for gu, dn in sets:
+        descs += [pkg.linear_desc(pkg.F16, m, 2 * it, hid, x, gu, act, flags=pkg.EPI_SILU_MUL),
+                  pkg.linear_desc(pkg.F16, m, hid, it, act, dn, x, flags=pkg.ACCUMULATE)]
+    warm = host.time_linears_each(ctx, descs[:2], 20, 400)
+    cold = host.time_linears_each(ctx, descs, 20, 416)
+    pair = lambda ms: ms[0::2] + ms[1::2]  # noqa: E731
+    f = 2 * m * 2 * it * hid + 2 * m * hid * it
+    out = {"warm": dist(pair(warm)), "cold": dist(pair(cold)),
+           "gu_cold": dist(cold[0::2]), "down_cold": dist(cold[1::2])}
+    out["tflops_cold_median"] = round(f / (out["cold"]["median"] * 1e-6) / 1e12, 1)
+    for b in [x, act] + [b for s in sets for b in s]:
+        b.free()
+    return out
+
+
 def dec_layer_flops(s):
     """Per-layer FLOPs of a prefill of s tokens: the four projections plus the
     causal attention (QK^T and PV over the s(s+1)/2 visible pairs per head)."""
@@ -337,6 +476,13 @@ def main():
                     help="only the config-5 aligner forward (for profiling); prints its detail")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 512 MiB copy 3 times (calibrates FETCH_SIZE/WRITE_SIZE)")
+    ap.add_argument("--site", default=None,
+                    help="only launch one GEMM site --launches times (for rocprofv3 counter runs): "
+                         "qkv, o, gu, down (fused), q, k, v, gate, up (unfused) over the 28 layers' "
+                         "weights, or config1")
+    ap.add_argument("--launches", type=int, default=56)
+    ap.add_argument("--warm", action="store_true",
+                    help="with --site: repeat layer 0's (or config 1's first) W instead of cycling")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -353,6 +499,23 @@ def main():
         with pkg.Context(0) as ctx:
             host.copy_calibration(ctx, COPY_CAL_BYTES, 3)
         log(f"[bench] copied {COPY_CAL_BYTES} bytes x3")
+        return
+
+    if args.site:
+        with pkg.Context(0) as ctx:
+            if args.site == "config1":
+                m, n, k = 256, 3072, 1024
+                a = ctx.to_device(host.synth_normal(0, 11, (m, k)))
+                c = ctx.alloc(m * n * 2)
+                ws = [ctx.to_device(host.synth_normal(0, 12 if i == 0 else 1200 + i, (n, k), 0, 0.02))
+                      for i in range(1 if args.warm else 48)]
+                descs = [pkg.linear_desc(pkg.F16, m, n, k, a, w, c) for w in ws]
+            else:
+                unf = args.site in dec_sites(True) and args.site not in dec_sites(False)
+                ss = SiteSet(pkg, host, ctx, 1024, 1 if args.warm else DEC["layers"], unf)
+                descs = ss.descs[args.site]
+            ms = host.time_linears_each(ctx, descs, 0, args.launches)
+            print(json.dumps({"site": args.site, "warm": args.warm, "per_launch": dist(ms)}), flush=True)
         return
 
     if args.e2e_only:
@@ -407,6 +570,19 @@ def main():
         detail["config2_tflops"] = round(f2 / (t2 * 1e-3) / 1e12, 1)
         for b in (dx, dgu, dwd, dact):
             b.free()
+        # the per-launch protocol: each config-3 site fused and unfused, cold and
+        # warm, and configs 1 and 2 cold and warm
+        for unf, key in ((False, "config3_sites_protocol"), (True, "config3_unfused_protocol")):
+            ss = SiteSet(pkg, host, ctx, m, DEC["layers"], unf)
+            sites_d, step_d = site_protocol(host, ctx, ss)
+            ss.close()
+            detail[key] = {"sites": sites_d, **step_d}
+            log(f"[bench] {key}: {step_d}; " +
+                ", ".join(f"{s} {v['cold']['median']}/{v['warm']['median']} us" for s, v in sites_d.items()))
+        detail["config1_protocol"] = config1_protocol(pkg, host, ctx)
+        detail["config2_protocol"] = config2_protocol(pkg, host, ctx)
+        log(f"[bench] config1: {detail['config1_protocol']}")
+        log(f"[bench] config2: {detail['config2_protocol']}")
     dec.close()
     if tdec is not None:
         # whole decoder layers: config 3's 1024 tokens and config 5's prefill length

@@ -276,6 +276,13 @@ void qah_ckpt_close(qah_ckpt* c);
 int qah_time_linear(qa_ctx* ctx, const qa_linear_desc* desc, int warmup, int iters,
                     double* ms_per_launch);
 
+/* `iters` back-to-back launches cycling through descs[0..ndesc), an event
+ * recorded before each launch and after the last on the context's stream:
+ * ms_each[i] is launch i's duration including its share of the launch gap
+ * (the per-launch figures whose median / p10 / p90 the benchmark reports). */
+int qah_time_linears_each(qa_ctx* ctx, const qa_linear_desc* descs, int ndesc, int warmup,
+                          int iters, float* ms_each);
+
 /* A plain 16-byte-per-thread copy of `bytes` between two fresh buffers,
  * `reps` times: the known-size reference that calibrates the FETCH_SIZE /
  * WRITE_SIZE counters. */

@@ -12,15 +12,20 @@ sample is exact) against the f64-exact oracle (or_linear with EXACT):
     GELU outputs, each one rounding of the exact value: within 1 ulp;
   * the residual stream after 2 layers (o + bias and fc2 + bias accumulated
     onto it, four roundings): the oracle chain run step by step on the same
-    inputs, within 2 ulps and >= 99% bit-identical (a tie rounded the other
-    way in one step carries into the next).
+    inputs.  Each step rounds h_i = r(h_{i-1} + y_i) once, so a difference
+    of at most half an ulp of |h_i| (plus the f32 accumulation error, far
+    smaller) enters per step and is carried into the next: elementwise
+    |got - want| <= sum_i ulp(|h_i|) <= 4 ulp(max_i |h_i|).  Where the chain
+    cancels (|h| small after adding y), that is many ulps of the result,
+    which is why the single-op relative metric does not apply here; the
+    north star's MAE does, and >= 99% of the outputs are bit-identical.
 """
 from __future__ import annotations
 
 import numpy as np
 import pytest
 
-from conftest import assert_parity
+from conftest import assert_parity, parity_stats, ulp16
 
 pytestmark = pytest.mark.gpu
 
@@ -65,10 +70,18 @@ def test_config4_encoder_linear_stack_bf16(ctx, pkg, orc):
                           bias=last["fc1"][1])
     assert_parity(got["act"][rows], want_act, orc, dt, ulp_tol=1)
     h = h0[rows].copy()
+    f = lambda bits: orc.h16_to_f32(bits, dt).astype(np.float64)  # noqa: E731
+    big = np.abs(f(h))
     for l in layers:
         h = orc.linear(dt, attn[rows], l["o"][0], h, flags=orc.ACCUMULATE | ex, bias=l["o"][1])
+        big = np.maximum(big, np.abs(f(h)))
         act = orc.linear(dt, norm2[rows], l["fc1"][0], z(F), flags=orc.EPI_GELU | ex,
                          bias=l["fc1"][1])
         h = orc.linear(dt, act, l["fc2"][0], h, flags=orc.ACCUMULATE | ex, bias=l["fc2"][1])
-    s = assert_parity(got["h"][rows], h, orc, dt, ulp_tol=2, mae_tol=8e-3)
-    assert s["identical"] >= 0.99, s
+        big = np.maximum(big, np.abs(f(h)))
+    err = np.abs(f(got["h"][rows]) - f(h))
+    bound = 2 * LAYERS * ulp16(big, dt)
+    worst = np.unravel_index(np.argmax(err - bound), err.shape)
+    assert (err <= bound).all(), (worst, err[worst], bound[worst])
+    s = parity_stats(got["h"][rows], h, orc, dt)
+    assert s["finite"] and s["mae"] <= 8e-3 and s["identical"] >= 0.99, s
