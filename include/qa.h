@@ -156,6 +156,18 @@ int qa_linear(qa_ctx* ctx, const qa_linear_desc* desc);
 /* Validate a descriptor without a device or a launch (the size guards of
  * src/decoder.rs:927-950 and src/audio_encoder_gpu.rs:216-245). */
 int qa_linear_validate(const qa_linear_desc* desc);
+/* qa_linear without any allocation, for callers that cannot call hipMalloc
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * allocation).  No counterpart in the reference.  Same descriptor, kernels
+ * and results as qa_linear; where qa_linear would grow its context's
+ * workspace for split-K partials, this keeps them in a file-scope device
+ * array of qa_linear_noalloc_scratch_floats() f32 (16 MiB), one per GPU,
+ * held until the process ends.  The planner never picks a split whose
+ * partials exceed it; a split forced larger (QA_SPLITS) is refused with
+ * QA_EINVAL.  All calls on one GPU share that GPU's array: calls that overlap
+ * on one GPU (contexts whose streams run at the same time) race on it. */
+int qa_linear_noalloc(qa_ctx* ctx, const qa_linear_desc* desc);
+size_t qa_linear_noalloc_scratch_floats(void);
 /* Launch the MLP block (see qa_mlp_desc). */
 int qa_mlp_fused(qa_ctx* ctx, const qa_mlp_desc* desc);
 

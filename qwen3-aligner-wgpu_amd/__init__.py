@@ -276,6 +276,7 @@ class HeadDesc(ctypes.Structure):
 EXPORTS = (
     "qa_ctx_create", "qa_ctx_destroy", "qa_ctx_stream", "qa_alloc", "qa_free",
     "qa_upload", "qa_download", "qa_sync", "qa_linear", "qa_linear_validate",
+    "qa_linear_noalloc", "qa_linear_noalloc_scratch_floats",
     "qa_mlp_fused", "qa_rms_norm", "qa_qk_norm_rope", "qa_attention_prefill",
     "qa_layer_norm", "qa_window_attention", "qa_add_position_table", "qa_conv2d_3x3s2",
     "qa_mel_filterbank", "qa_log_mel", "qa_rope_tables", "qa_embed_scatter", "qa_timestamp_head",
@@ -298,12 +299,15 @@ def lib() -> ctypes.CDLL:
         L.qa_ctx_destroy.argtypes = [vp]
         L.qa_ctx_stream.argtypes = [vp]
         L.qa_ctx_stream.restype = vp
+        L.qa_linear_noalloc_scratch_floats.argtypes = []
+        L.qa_linear_noalloc_scratch_floats.restype = sz
         L.qa_alloc.argtypes = [vp, sz, ctypes.POINTER(vp)]
         L.qa_free.argtypes = [vp, vp]
         L.qa_upload.argtypes = [vp, vp, sz, vp, sz]
         L.qa_download.argtypes = [vp, vp, vp, sz, sz]
         L.qa_sync.argtypes = [vp]
         L.qa_linear.argtypes = [vp, ctypes.POINTER(LinearDesc)]
+        L.qa_linear_noalloc.argtypes = [vp, ctypes.POINTER(LinearDesc)]
         L.qa_linear_validate.argtypes = [ctypes.POINTER(LinearDesc)]
         L.qa_mlp_fused.argtypes = [vp, ctypes.POINTER(MlpDesc)]
         L.qa_rms_norm.argtypes = [vp, ctypes.POINTER(RmsNormDesc)]
@@ -416,6 +420,11 @@ class Context:
 
     def linear(self, desc: LinearDesc) -> None:
         check(lib().qa_linear(self.handle, ctypes.byref(desc)))
+
+    def linear_noalloc(self, desc: LinearDesc) -> None:
+        """qa_linear_noalloc: qa_linear with split-K partials in the library's
+        fixed device scratch (no allocation)."""
+        check(lib().qa_linear_noalloc(self.handle, ctypes.byref(desc)))
 
     def mlp_fused(self, desc: MlpDesc) -> None:
         check(lib().qa_mlp_fused(self.handle, ctypes.byref(desc)))

@@ -13,6 +13,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -26,7 +27,20 @@ struct qa_ctx {
   int num_cus = 256;
   float* ws = nullptr;  // split-K partials
   size_t ws_floats = 0;
+  float* scratch = nullptr;  // this device's copy of `scratch` (qa_linear_noalloc)
 };
+
+// The allocation-free linear's split-K partials (qa_linear_noalloc): one
+// file-scope device array, 16 MiB of f32, which every GPU the library runs on
+// holds until the process ends.  Host code never passes its name to a kernel
+// (on the host the name is a stand-in, not a device address): each device's
+// address comes from hipGetSymbolAddress at context creation, with that
+// device current, and is kept per device.  Every qa_linear_noalloc call on a
+// GPU shares that GPU's array, so calls that overlap on one GPU (two contexts'
+// streams running at once) race on it.  Each split-K launch writes every
+// partial it later reads, so nothing needs clearing between calls.
+constexpr size_t kScratchFloats = (size_t)4 << 20;
+static __device__ __align__(256) float scratch[kScratchFloats];
 
 namespace {
 
@@ -155,7 +169,7 @@ constexpr double kReduceGBs = 3000.0;   // split-K reduce kernel, partials from 
 // where rounds = ceil(units / CUs); the cheapest candidate wins.
 void choose_group_m(qa::Plan& pl, int64_t span = 0);
 
-qa::Plan plan_linear(const qa_linear_desc& d, int num_cus) {
+qa::Plan plan_linear(const qa_linear_desc& d, int num_cus, size_t max_ws_floats = SIZE_MAX) {
   qa::Plan pl{};
   const bool silu = d.flags & QA_EPI_SILU_MUL;
   pl.epi = silu ? qa::EPI_SILU : (d.flags & QA_EPI_GELU) ? qa::EPI_GELU : qa::EPI_PLAIN;
@@ -191,6 +205,9 @@ qa::Plan plan_linear(const qa_linear_desc& d, int num_cus) {
       int64_t kchunk = ((K + want - 1) / want + 63) / 64 * 64;
       const int64_t splits = (K + kchunk - 1) / kchunk;
       if (splits > 1 && kchunk < 256 && forced_splits <= 0) break;  // keep >= 4 stages per split
+      // partials that would not fit the caller's workspace bound (the
+      // allocation-free entry point's scratch) rule a split count out
+      if (splits > 1 && forced_splits <= 0 && (size_t)(splits * M * N) > max_ws_floats) break;
       const int64_t units = tiles * splits;
       const int64_t rounds = (units + num_cus - 1) / num_cus;
       double cost = (double)rounds * (kTileFixedUs + (double)kchunk / 64.0 * stage_us(cands[ci]));
@@ -307,9 +324,62 @@ int ensure_workspace(qa_ctx* ctx, size_t floats) {
   return ok();
 }
 
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch[kMaxDevices] = {};
+
+// This device's address of `scratch`; the device must be current.
+int scratch_address(int device, float** out) {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (device < 0 || device >= kMaxDevices)
+    return fail(QA_EUNSUPPORTED, "device %d: at most %d devices", device, kMaxDevices);
+  if (!g_scratch[device]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    g_scratch[device] = (float*)p;
+  }
+  *out = g_scratch[device];
+  return ok();
+}
+
 int set_device(qa_ctx* ctx) {
   const hipError_t e = hipSetDevice(ctx->device);
   return e == hipSuccess ? ok() : hip_fail(e, "hipSetDevice");
+}
+
+// Launch a validated, planned projection with split-K partials in `ws`.
+int launch_linear(qa_ctx* ctx, const qa_linear_desc* d, const qa::Plan& plan, float* ws) {
+  qa::GemmParams p{};
+  p.a = (const uint16_t*)d->a;
+  p.w = (const uint16_t*)d->w;
+  p.c = (uint16_t*)d->c;
+  p.bias = (const uint16_t*)d->bias;
+  p.ws = ws;
+  p.a_bytes = (int)(((d->m - 1) * d->lda + d->k) * 2);
+  p.w_bytes = (int)((((d->flags & QA_TRANSB) ? d->k : d->n) - 1) * d->ldb +
+                    ((d->flags & QA_TRANSB) ? d->n : d->k)) * 2;
+  p.M = (int)d->m;
+  p.N = (int)d->n;
+  p.K = (int)d->k;
+  p.lda = (int)d->lda;
+  p.ldb = (int)d->ldb;
+  p.ldc = (int)d->ldc;
+  p.bsa = d->bsa;
+  p.bsb = d->bsb;
+  p.bsc = d->bsc;
+  p.tiles_m = plan.tiles_m;
+  p.tiles_n = plan.tiles_n;
+  p.splits = plan.splits;
+  p.kchunk = plan.kchunk;
+  p.accumulate = (d->flags & QA_ACCUMULATE) ? 1 : 0;
+  p.bias_rows = (d->flags & QA_BIAS_ROWS) ? 1 : 0;
+  p.group_m = plan.group_m;
+  const int batch = d->batch > 0 ? (int)d->batch : 1;
+  if (plan.splits > 1 && batch > 1)
+    return fail(QA_EUNSUPPORTED, "qa_linear: split-K with batch > 1");
+  const hipError_t e = qa::launch_gemm((int)d->dtype, plan, p, batch, ctx->stream);
+  return e == hipSuccess ? ok() : hip_fail(e, "qa_linear launch");
 }
 
 }  // namespace
@@ -341,6 +411,10 @@ int qa_ctx_create(int device, qa_ctx** out) {
   qa_ctx* ctx = new qa_ctx;
   ctx->device = device;
   ctx->num_cus = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
+  if (int rc = scratch_address(device, &ctx->scratch)) {
+    delete ctx;
+    return rc;
+  }
   e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
   if (e != hipSuccess) {
     delete ctx;
@@ -420,6 +494,7 @@ int qa_sync(qa_ctx* ctx) {
 
 int qa_linear_validate(const qa_linear_desc* desc) { return validate(desc); }
 
+
 int qa_linear(qa_ctx* ctx, const qa_linear_desc* d) {
   if (!ctx) return fail(QA_EINVAL, "qa_linear: null context");
   if (int rc = validate(d)) return rc;
@@ -429,37 +504,26 @@ int qa_linear(qa_ctx* ctx, const qa_linear_desc* d) {
   if (plan.splits > 1) {
     if (int rc = ensure_workspace(ctx, plan.ws_floats)) return rc;
   }
-  qa::GemmParams p{};
-  p.a = (const uint16_t*)d->a;
-  p.w = (const uint16_t*)d->w;
-  p.c = (uint16_t*)d->c;
-  p.bias = (const uint16_t*)d->bias;
-  p.ws = ctx->ws;
-  p.a_bytes = (int)(((d->m - 1) * d->lda + d->k) * 2);
-  p.w_bytes = (int)((((d->flags & QA_TRANSB) ? d->k : d->n) - 1) * d->ldb +
-                    ((d->flags & QA_TRANSB) ? d->n : d->k)) * 2;
-  p.M = (int)d->m;
-  p.N = (int)d->n;
-  p.K = (int)d->k;
-  p.lda = (int)d->lda;
-  p.ldb = (int)d->ldb;
-  p.ldc = (int)d->ldc;
-  p.bsa = d->bsa;
-  p.bsb = d->bsb;
-  p.bsc = d->bsc;
-  p.tiles_m = plan.tiles_m;
-  p.tiles_n = plan.tiles_n;
-  p.splits = plan.splits;
-  p.kchunk = plan.kchunk;
-  p.accumulate = (d->flags & QA_ACCUMULATE) ? 1 : 0;
-  p.bias_rows = (d->flags & QA_BIAS_ROWS) ? 1 : 0;
-  p.group_m = plan.group_m;
-  const int batch = d->batch > 0 ? (int)d->batch : 1;
-  if (plan.splits > 1 && batch > 1)
-    return fail(QA_EUNSUPPORTED, "qa_linear: split-K with batch > 1");
-  const hipError_t e = qa::launch_gemm((int)d->dtype, plan, p, batch, ctx->stream);
-  return e == hipSuccess ? ok() : hip_fail(e, "qa_linear launch");
+  return launch_linear(ctx, d, plan, ctx->ws);
 }
+
+int qa_linear_noalloc(qa_ctx* ctx, const qa_linear_desc* d) {
+  if (!ctx) return fail(QA_EINVAL, "qa_linear_noalloc: null context");
+  if (int rc = validate(d)) return rc;
+  if (d->m == 0) return ok();
+  if (int rc = set_device(ctx)) return rc;
+  // split counts whose partials exceed the scratch are never planned; only a
+  // split forced through QA_SPLITS can ask for more
+  const qa::Plan plan = plan_linear(*d, ctx->num_cus, kScratchFloats);
+  if (plan.splits > 1 && plan.ws_floats > kScratchFloats)
+    return fail(QA_EINVAL,
+                "qa_linear_noalloc: %d K splits of a %lld x %lld output need %zu f32 partials; the "
+                "scratch holds %zu",
+                plan.splits, (long long)d->m, (long long)d->n, plan.ws_floats, kScratchFloats);
+  return launch_linear(ctx, d, plan, ctx->scratch);
+}
+
+size_t qa_linear_noalloc_scratch_floats(void) { return kScratchFloats; }
 
 int qa_mlp_fused(qa_ctx* ctx, const qa_mlp_desc* d) {
   if (!ctx || !d) return fail(QA_EINVAL, "qa_mlp_fused: null argument");
