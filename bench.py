@@ -117,6 +117,7 @@ def cpu_baseline(orc, host, m, budget_s):
         t1 = time.perf_counter() - t0
     finally:
         orc.set_threads(threads)
+    per_config = cpu_other_configs(orc, host)
     cpu_model = ""
     try:
         for line in open("/proc/cpuinfo"):
@@ -139,7 +140,105 @@ def cpu_baseline(orc, host, m, budget_s):
         "cpu_model": cpu_model,
         "nproc": os.cpu_count(),
         "omp_num_threads": os.environ.get("OMP_NUM_THREADS"),
+        "per_config": per_config,
     }
+
+
+def cpu_other_configs(orc, host):
+    """The oracle on BASELINE configs 1, 2 and 4 and a bounded sample of
+    config 5, on the same threads: config 1 and 2 whole; config 4 as one
+    encoder layer at M = 3750 (bf16; qkv, o, fc1 + GELU, fc2) plus the conv
+    GEMM, extrapolated to 18 layers; config 5 as one decoder layer at
+    s = 4334 (norms, projections, RoPE, causal attention), one tower layer
+    at 3900 tokens with the post-projection, and the conv stem over 10 of the
+    300 chunks, extrapolated to 28 decoder layers, 18 tower layers and 300
+    chunks (the log-mel and the head are left out: under 1% of the forward).
+    The decoder layer's causal attention is timed on its last 512 query rows
+    (exact for those rows) and scaled by the causal area those rows cover."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from chains import EPS, HD, INTER, NKVH, NQH, oracle_tower, perm_conv
+    from qwen3_aligner_wgpu_amd import synthetic as syn
+    out, z = {}, lambda r, c: np.zeros((r, c), np.uint16)  # noqa: E731
+    # config 1
+    a, w = host.synth_normal(0, 11, (256, 1024)), host.synth_normal(0, 12, (3072, 1024), 0, 0.02)
+    t0 = time.perf_counter()
+    for _ in range(5):
+        orc.linear(0, a, w, z(256, 3072))
+    t = (time.perf_counter() - t0) / 5
+    out["config1"] = {"ms": round(t * 1e3, 2), "tflops": round(2 * 256 * 3072 * 1024 / t / 1e12, 4)}
+    # config 2
+    x = host.synth_normal(0, 21, (512, 1024))
+    wgu, wd = host.synth_normal(0, 22, (6144, 1024), 0, 0.02), host.synth_normal(0, 23, (1024, 3072), 0, 0.02)
+    t0 = time.perf_counter()
+    act = orc.linear(0, x, wgu, z(512, 3072), flags=orc.EPI_SILU_MUL)
+    orc.linear(0, act, wd, x.copy(), flags=orc.ACCUMULATE)
+    t = time.perf_counter() - t0
+    out["config2"] = {"ms": round(t * 1e3, 2), "tflops": round(9.664e9 / t / 1e12, 4)}
+    # config 4: one layer + the conv GEMM, extrapolated
+    m, d, f, ck = 3750, ENC["d_model"], ENC["ffn"], ENC["conv_k"]
+    g = lambda tid, shp, std: host.synth_normal(1, tid, shp, 0.0, std, 1)  # noqa: E731
+    xin, h = g(2, (m, d), 1.0), g(5, (m, d), 1.0)
+    t0 = time.perf_counter()
+    orc.linear(1, g(1, (m, ck), 1.0), g(4000, (d, ck), 0.02), z(m, d), flags=orc.EPI_GELU,
+               bias=g(4001, (d,), 0.01))
+    tc = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    orc.linear(1, xin, g(5000, (3 * d, d), 0.02), z(m, 3 * d), bias=g(5001, (3 * d,), 0.01))
+    h = orc.linear(1, xin, g(5002, (d, d), 0.02), h, flags=orc.ACCUMULATE, bias=g(5003, (d,), 0.01))
+    act = orc.linear(1, xin, g(5004, (f, d), 0.02), z(m, f), flags=orc.EPI_GELU, bias=g(5005, (f,), 0.01))
+    orc.linear(1, act, g(5006, (d, f), 0.02), h, flags=orc.ACCUMULATE, bias=g(5007, (d,), 0.01))
+    tl = time.perf_counter() - t0
+    t4 = tc + ENC["layers"] * tl
+    out["config4"] = {"ms_extrapolated": round(t4 * 1e3, 1),
+                      "tflops": round(1308.3e9 / t4 / 1e12, 4),
+                      "sample": f"conv GEMM {tc:.2f} s + one layer {tl:.2f} s, x 18 layers"}
+    # config 5 sample
+    w5 = syn.aligner_weights(0, 1, 1, 5)
+    s = 4334
+    hd_in = host.synth_normal(5, 9, (s, 1024))
+    cap = (s + 63) // 64 * 64
+    import __graft_entry__ as entry
+    cos, sin = entry.load_package().rope_tables(cap, 128, 1e6, 0)
+    lw = w5["dec"][0]
+    t0 = time.perf_counter()
+    normed = orc.rms_norm(0, hd_in, lw["iln"], EPS)
+    qkv_w = np.ascontiguousarray(np.concatenate([lw["q"], lw["k"], lw["v"]]))
+    qkv = orc.linear(0, normed, qkv_w, z(s, qkv_w.shape[0]))
+    kc, vc = np.zeros((NKVH, cap, HD), np.uint16), np.zeros((NKVH, HD, cap), np.uint16)
+    q = orc.qk_norm_rope(0, qkv, NQH, NKVH, HD, lw["qn"], lw["kn"], cos, sin, 0, EPS, kc, vc, 0)
+    t_lin = time.perf_counter() - t0
+    tail = 512
+    t0 = time.perf_counter()
+    attn = orc.attention(0, np.ascontiguousarray(q[:, s - tail:]), kc, vc, s - tail)
+    t_att = (time.perf_counter() - t0) * (s * (s + 1) / 2) / (tail * (2 * s - tail + 1) / 2)
+    attn = np.ascontiguousarray(np.concatenate([np.zeros((s - tail, attn.shape[1]), np.uint16), attn]))
+    t0 = time.perf_counter()
+    h2 = orc.linear(0, attn, lw["o"], hd_in.copy(), flags=orc.ACCUMULATE)
+    norm2 = orc.rms_norm(0, h2, lw["pln"], EPS)
+    gu_w = np.ascontiguousarray(np.concatenate([lw["gate"], lw["up"]]))
+    act = orc.linear(0, norm2, gu_w, z(s, INTER), flags=orc.EPI_SILU_MUL)
+    orc.linear(0, act, lw["down"], h2, flags=orc.ACCUMULATE)
+    t_lin += time.perf_counter() - t0
+    t_dec = t_lin + t_att
+    n_tok = 3900
+    t0 = time.perf_counter()
+    oracle_tower(orc, 0, w5["enc"], None, n_tok, start="h", h0=host.synth_normal(5, 10, (n_tok, 896)))
+    t_tow = time.perf_counter() - t0
+    b = 10
+    mel = host.synth_normal(5, 11, (b, 128, 100, 1), 0, 1.0)
+    (c1w, c1b), (c2w, c2b), (c3w, c3b) = w5["enc"]["conv"]
+    t0 = time.perf_counter()
+    y1 = orc.conv3x3s2(0, mel, perm_conv(c1w), c1b)
+    y2 = orc.conv3x3s2(0, y1.reshape(b, 64, 50, 480), perm_conv(c2w), c2b)
+    orc.conv3x3s2(0, y2.reshape(b, 32, 25, 480), perm_conv(c3w), c3b, token_major=True)
+    t_stem = time.perf_counter() - t0
+    t5 = 28 * t_dec + 18 * t_tow + 30 * t_stem
+    out["config5"] = {"s_extrapolated": round(t5, 1),
+                      "sample": f"one decoder layer at s={s} {t_dec:.1f} s (attention {t_att:.1f} s "
+                                f"scaled from its last {tail} rows), one tower layer + "
+                                f"post at {n_tok} tokens {t_tow:.1f} s, stem over {b} chunks "
+                                f"{t_stem:.1f} s; x 28, x 18, x 30"}
+    return out
 
 
 def bench_decoder(pkg, host, ctx, m, warmup, steps, tdec=None):

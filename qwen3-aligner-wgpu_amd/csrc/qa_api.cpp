@@ -156,9 +156,17 @@ double stage_us(int tile) {
     case qa::TILE_128x192: return 0.72;
     case qa::TILE_64x128: return 0.36;
     case qa::TILE_64x64: return 0.25;
+    case qa::TILE_64x64_P2: return 0.21;
     case qa::TILE_256x256: return 1.75;
     default: return 0.56;
   }
+}
+// 64-deep planes per ring stage: a split's k range runs in whole stages (the
+// planes past its end read zeros), so its cost rounds up to that multiple.
+int planes(int tile) { return tile == qa::TILE_64x64_P2 ? 2 : 1; }
+double stages_of(int tile, int64_t kchunk) {
+  const int64_t pl = planes(tile);
+  return (double)(((kchunk + 63) / 64 + pl - 1) / pl * pl);
 }
 constexpr double kTileFixedUs = 3.0;
 constexpr double kLaunchUs = 2.0;       // one more kernel in the stream (split-K reduce)
@@ -187,7 +195,7 @@ qa::Plan plan_linear(const qa_linear_desc& d, int num_cus, size_t max_ws_floats 
 
   int cands[qa::TILE_COUNT] = {qa::TILE_128x128, qa::TILE_256x128, qa::TILE_128x256,
                                qa::TILE_64x128,  qa::TILE_64x64,   qa::TILE_128x192,
-                               qa::TILE_256x256};
+                               qa::TILE_256x256, qa::TILE_64x64_P2};
   int ncand = qa::TILE_COUNT;
   if (pl.transb) ncand = 1;  // the conv operand path has one tile shape
   if (forced_tile >= 0 && forced_tile < qa::TILE_COUNT && !pl.transb) {
@@ -210,7 +218,7 @@ qa::Plan plan_linear(const qa_linear_desc& d, int num_cus, size_t max_ws_floats 
       if (splits > 1 && forced_splits <= 0 && (size_t)(splits * M * N) > max_ws_floats) break;
       const int64_t units = tiles * splits;
       const int64_t rounds = (units + num_cus - 1) / num_cus;
-      double cost = (double)rounds * (kTileFixedUs + (double)kchunk / 64.0 * stage_us(cands[ci]));
+      double cost = (double)rounds * (kTileFixedUs + stages_of(cands[ci], kchunk) * stage_us(cands[ci]));
       if (splits > 1)
         cost += kLaunchUs + (double)(splits * 4 + 2) * (double)M * (double)N / (kReduceGBs * 1e3);
       if (cost < best * 0.999) {

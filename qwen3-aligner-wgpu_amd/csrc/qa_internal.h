@@ -24,6 +24,7 @@ enum TileCfg : int {
   TILE_64x64 = 4,    // waves of 32(m) x 64(n)
   TILE_128x192 = 5,  // waves of 64(m) x 96(n)
   TILE_256x256 = 6,  // one k group of 2x4 waves of 128(m) x 64(n)
+  TILE_64x64_P2 = 7, // 64x64 with two 64-deep planes per ring stage (one barrier per 128 k)
   TILE_COUNT
 };
 
@@ -35,7 +36,8 @@ inline TileShape tile_shape(int cfg) {
     case TILE_256x128: return {256, 128};
     case TILE_128x256: return {128, 256};
     case TILE_64x128: return {64, 128};
-    case TILE_64x64: return {64, 64};
+    case TILE_64x64:
+    case TILE_64x64_P2: return {64, 64};
     case TILE_128x192: return {128, 192};
     case TILE_256x256: return {256, 256};
     default: return {128, 128};

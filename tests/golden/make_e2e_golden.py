@@ -46,6 +46,14 @@ def digest(a: np.ndarray) -> str:
     return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()[:16]
 
 
+def rows_distance(a_bits, b_bits):
+    """MAE and relative RMS between two sets of f16 rows (b the reference)."""
+    a = a_bits.view(np.float16).astype(np.float64)
+    b = b_bits.view(np.float16).astype(np.float64)
+    d = a - b
+    return dict(mae=float(np.abs(d).mean()), rel_rms=float(np.sqrt((d ** 2).mean() / (b ** 2).mean())))
+
+
 def summary(r, topk=TOPK):
     """Per-slot results of one oracle forward: json-able lists + arrays."""
     lg = r["logits"]
@@ -116,6 +124,7 @@ def main():
         d = a16 - a32
         out["tower16_vs_cpu_ref"] = dict(mae=float(np.abs(d).mean()),
                                          rel_rms=float(np.sqrt((d ** 2).mean() / (a32 ** 2).mean())))
+        out["rows16_vs_cpu_ref"] = rows_distance(ar16["rows"], arc["rows"])
         log(f"cpu_ref done: tower distance {out['tower16_vs_cpu_ref']}")
     out["seconds_cpu"] = round(time.time() - t0, 1)
     path = os.path.join(HERE, f"e2e_{args.tag}.json")

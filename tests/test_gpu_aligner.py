@@ -129,8 +129,9 @@ def test_aligner_e2e_300s_against_fixture(ctx, pkg, orc):
         rows allow (logits_gate);
       * the classes identical at every slot with a clear oracle margin;
       * against the reference CPU path's forward (f32 tower, cpu_ref): the
-        rows by the north star's MAE, the classes identical at clear slots,
-        the relative RMS reported."""
+        rows no further from it than the oracle's 16-bit chain is (the
+        reference GPU path's rounding points put it 1.3e-3 relative RMS away)
+        plus one ulp, and the classes identical at clear slots."""
     from qwen3_aligner_wgpu_amd import synthetic as syn
     from chains import logits_gate, rows_gate
     path = os.path.join(HERE, "golden", "e2e_300s")
@@ -170,7 +171,8 @@ def test_aligner_e2e_300s_against_fixture(ctx, pkg, orc):
     same_ref = g["classes"] == want_ref
     print(f"e2e 300 s vs the reference CPU path (f32 tower): rows {st_ref}; classes identical at "
           f"{same_ref.sum()}/{want_ref.size} slots ({clear_ref.sum()} clear)")
-    assert st_ref["mae"] <= 1e-3, st_ref
+    base = gold["rows16_vs_cpu_ref"]
+    assert st_ref["rel_rms"] <= base["rel_rms"] + 2.0 ** -10, (st_ref, base)
     assert same_ref[clear_ref].all(), np.nonzero(~same_ref & clear_ref)
 
 
