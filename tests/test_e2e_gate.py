@@ -77,6 +77,9 @@ def test_gates_reject_a_planted_mistake(orc, tiny, tower, skip, prefix):
     r = run(tower=tower, skip=skip)
     ok_rows, st, _, _ = _gates(orc, r, gold, arr, w, prefix)
     assert not ok_rows, st
+    # far outside the looser bound the 300 s test derives from two correct
+    # forwards (twice their 1.3e-3 relative RMS distance)
+    assert st["rel_rms"] > 50 * 2 * 1.3e-3, st
 
 
 def test_logits_gate_rejects_a_shifted_row(orc, tiny):

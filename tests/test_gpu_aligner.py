@@ -124,14 +124,19 @@ def test_aligner_e2e_300s_against_fixture(ctx, pkg, orc):
     """BASELINE config 5 against the oracle's forward of the same seeded
     inputs (tests/golden/e2e_300s.json / .npz):
       * the final hidden rows at the 240 <timestamp> slots against the 16-bit
-        chain's (rows_gate: MAE and one ulp of relative RMS);
+        chain's (rows_gate).  After 18 + 28 layers of 16-bit arithmetic two
+        correct forwards drift apart by more than an ulp: the oracle's own
+        16-bit-tower and f32-tower forwards are 1.3e-3 relative RMS apart
+        (rows16_vs_cpu_ref in the fixture).  The GPU, which rounds where the
+        16-bit chain does, may differ from it by at most twice that distance
+        in relative RMS and MAE; a wiring mistake moves the rows by orders of
+        magnitude more (tests/test_e2e_gate.py);
       * the logits at each slot's 8 best labels within what the two sets of
         rows allow (logits_gate);
       * the classes identical at every slot with a clear oracle margin;
       * against the reference CPU path's forward (f32 tower, cpu_ref): the
-        rows no further from it than the oracle's 16-bit chain is (the
-        reference GPU path's rounding points put it 1.3e-3 relative RMS away)
-        plus one ulp, and the classes identical at clear slots."""
+        rows within twice the oracle chains' distance, and the classes
+        identical at clear slots."""
     from qwen3_aligner_wgpu_amd import synthetic as syn
     from chains import logits_gate, rows_gate
     path = os.path.join(HERE, "golden", "e2e_300s")
@@ -150,7 +155,9 @@ def test_aligner_e2e_300s_against_fixture(ctx, pkg, orc):
     assert dg(g["ids"]) == gold["digests"]["ids"]
     assert list(g["ts"]) == gold["ts"]
     rows = g["h"][g["ts"]]
-    ok, st = rows_gate(orc, c["dtype"], rows, arr["chain16_rows"])
+    drift = gold["rows16_vs_cpu_ref"]
+    ok, st = rows_gate(orc, c["dtype"], rows, arr["chain16_rows"],
+                       rel_rms_bound=2 * drift["rel_rms"], mae_bound=2 * drift["mae"])
     ok_lg, use = logits_gate(orc, c["dtype"], rows, g["logits"], arr["chain16_rows"],
                              arr["chain16_top_idx"], arr["chain16_top_logits"], w["norm_w"],
                              w["score"])
@@ -171,8 +178,7 @@ def test_aligner_e2e_300s_against_fixture(ctx, pkg, orc):
     same_ref = g["classes"] == want_ref
     print(f"e2e 300 s vs the reference CPU path (f32 tower): rows {st_ref}; classes identical at "
           f"{same_ref.sum()}/{want_ref.size} slots ({clear_ref.sum()} clear)")
-    base = gold["rows16_vs_cpu_ref"]
-    assert st_ref["rel_rms"] <= base["rel_rms"] + 2.0 ** -10, (st_ref, base)
+    assert st_ref["rel_rms"] <= 2 * drift["rel_rms"], (st_ref, drift)
     assert same_ref[clear_ref].all(), np.nonzero(~same_ref & clear_ref)
 
 
