@@ -168,6 +168,16 @@ int qa_linear_validate(const qa_linear_desc* desc);
  * on one GPU (contexts whose streams run at the same time) race on it. */
 int qa_linear_noalloc(qa_ctx* ctx, const qa_linear_desc* desc);
 size_t qa_linear_noalloc_scratch_floats(void);
+/* Name `bytes` of device memory at `ptr` -- normally the weights of the
+ * projection that follows -- for the NEXT projection launched on this context
+ * (qa_linear, qa_linear_noalloc, either GEMM of qa_mlp_fused) to pull from HBM
+ * into the memory-side cache while it computes, so the following launch
+ * starts on cached weights.  A hint only: results never depend on it, the
+ * launch that takes it over clears it, and a hint past what one launch
+ * touches (a few tens of MB) is cut short.  No counterpart in the reference;
+ * for layer loops that stream a model's weights once per step
+ * (src/decoder.rs:1321-1657 runs qkv, o, gate|up, down per layer). */
+int qa_prefetch_hint(qa_ctx* ctx, const void* ptr, size_t bytes);
 /* Launch the MLP block (see qa_mlp_desc). */
 int qa_mlp_fused(qa_ctx* ctx, const qa_mlp_desc* desc);
 

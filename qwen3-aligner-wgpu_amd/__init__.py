@@ -276,7 +276,7 @@ class HeadDesc(ctypes.Structure):
 EXPORTS = (
     "qa_ctx_create", "qa_ctx_destroy", "qa_ctx_stream", "qa_alloc", "qa_free",
     "qa_upload", "qa_download", "qa_sync", "qa_linear", "qa_linear_validate",
-    "qa_linear_noalloc", "qa_linear_noalloc_scratch_floats",
+    "qa_linear_noalloc", "qa_linear_noalloc_scratch_floats", "qa_prefetch_hint",
     "qa_mlp_fused", "qa_rms_norm", "qa_qk_norm_rope", "qa_attention_prefill",
     "qa_layer_norm", "qa_window_attention", "qa_add_position_table", "qa_conv2d_3x3s2",
     "qa_mel_filterbank", "qa_log_mel", "qa_rope_tables", "qa_embed_scatter", "qa_timestamp_head",
@@ -308,6 +308,7 @@ def lib() -> ctypes.CDLL:
         L.qa_sync.argtypes = [vp]
         L.qa_linear.argtypes = [vp, ctypes.POINTER(LinearDesc)]
         L.qa_linear_noalloc.argtypes = [vp, ctypes.POINTER(LinearDesc)]
+        L.qa_prefetch_hint.argtypes = [vp, vp, sz]
         L.qa_linear_validate.argtypes = [ctypes.POINTER(LinearDesc)]
         L.qa_mlp_fused.argtypes = [vp, ctypes.POINTER(MlpDesc)]
         L.qa_rms_norm.argtypes = [vp, ctypes.POINTER(RmsNormDesc)]
@@ -425,6 +426,13 @@ class Context:
         """qa_linear_noalloc: qa_linear with split-K partials in the library's
         fixed device scratch (no allocation)."""
         check(lib().qa_linear_noalloc(self.handle, ctypes.byref(desc)))
+
+    def prefetch_hint(self, buf, nbytes=None) -> None:
+        """qa_prefetch_hint: the next projection launched on this context pulls
+        `buf` (normally the following projection's weights) toward the caches."""
+        ptr = None if buf is None else buf.ptr
+        check(lib().qa_prefetch_hint(self.handle, ptr, 0 if buf is None else
+                                     (buf.nbytes if nbytes is None else nbytes)))
 
     def mlp_fused(self, desc: MlpDesc) -> None:
         check(lib().qa_mlp_fused(self.handle, ctypes.byref(desc)))

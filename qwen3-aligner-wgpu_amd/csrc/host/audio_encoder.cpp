@@ -35,9 +35,12 @@ int upload_f32(qa_ctx* ctx, const float* src, size_t n, Buffer* b) {
   return qa_upload(ctx, b->ptr, 0, src, n * 4);
 }
 
-// y = x W^T + bias (+ y with `acc`, GELU with `gelu`), rows m
+// y = x W^T + bias (+ y with `acc`, GELU with `gelu`), rows m; the launch
+// pulls `next`'s weights (the projection after it) toward the caches
 int linear(qa_ctx* ctx, int dtype, const void* x, const Linear& l, void* y, int64_t m,
-           bool acc, bool gelu) {
+           bool acc, bool gelu, const Linear* next = nullptr) {
+  if (next)
+    if (int rc = qa_prefetch_hint(ctx, next->w.ptr, next->w.bytes)) return rc;
   qa_linear_desc d{};
   d.dtype = (uint32_t)dtype;
   d.flags = (acc ? QA_ACCUMULATE : 0u) | (gelu ? QA_EPI_GELU : 0u);
@@ -208,7 +211,8 @@ int AudioEncoder::stem(int n_chunks, hipEvent_t* ev) {
 }
 
 int AudioEncoder::conv_out(int64_t n) {
-  if (int rc = linear(ctx, dtype, y3.ptr, co, h.ptr, n, false, false)) return rc;
+  if (int rc = linear(ctx, dtype, y3.ptr, co, h.ptr, n, false, false, layers ? &L[0].qkv : &p1))
+    return rc;
   qa_position_add_desc d{};
   d.dtype = (uint32_t)dtype;
   d.rows = n;
@@ -247,7 +251,8 @@ int AudioEncoder::layer(int li, int64_t n, hipEvent_t* ev) {
     return qa_layer_norm(ctx, &d);
   };
   run([&] { return ln(l.ln1_w, l.ln1_b); });
-  run([&] { return linear(ctx, dtype, normed.ptr, l.qkv, qkv.ptr, n, false, false); });
+  const Linear* after = li + 1 < layers ? &L[(size_t)li + 1].qkv : &p1;
+  run([&] { return linear(ctx, dtype, normed.ptr, l.qkv, qkv.ptr, n, false, false, &l.o); });
   run([&] {
     qa_window_attention_desc d{};
     d.dtype = (uint32_t)dtype;
@@ -261,10 +266,10 @@ int AudioEncoder::layer(int li, int64_t n, hipEvent_t* ev) {
     d.ldo = d_model;
     return qa_window_attention(ctx, &d);
   });
-  run([&] { return linear(ctx, dtype, attn.ptr, l.o, h.ptr, n, true, false); });
+  run([&] { return linear(ctx, dtype, attn.ptr, l.o, h.ptr, n, true, false, &l.fc1); });
   run([&] { return ln(l.ln2_w, l.ln2_b); });
-  run([&] { return linear(ctx, dtype, normed.ptr, l.fc1, act.ptr, n, false, true); });
-  run([&] { return linear(ctx, dtype, act.ptr, l.fc2, h.ptr, n, true, false); });
+  run([&] { return linear(ctx, dtype, normed.ptr, l.fc1, act.ptr, n, false, true, &l.fc2); });
+  run([&] { return linear(ctx, dtype, act.ptr, l.fc2, h.ptr, n, true, false, after); });
   return rc;
 }
 
@@ -281,7 +286,7 @@ int AudioEncoder::post(int64_t n) {
   d.ldy = d_model;
   d.eps = 1e-5f;
   if (int rc = qa_layer_norm(ctx, &d)) return rc;
-  if (int rc = linear(ctx, dtype, normed.ptr, p1, pact.ptr, n, false, true)) return rc;
+  if (int rc = linear(ctx, dtype, normed.ptr, p1, pact.ptr, n, false, true, &p2)) return rc;
   return linear(ctx, dtype, pact.ptr, p2, out.ptr, n, false, false);
 }
 

@@ -121,8 +121,12 @@ int TextDecoder::layer(int li, int rows, hipEvent_t* ev) {
   };
   // 1. input RMSNorm
   run([&] { return rms(l.iln, lin.normed.ptr); });
+  // Each projection pulls the next one's weights toward the caches while it
+  // runs (the down projection pulls the next layer's qkv weights).
+  auto next_w = [&](const Buffer& b) { return qa_prefetch_hint(ctx, b.ptr, b.bytes); };
   // 2. fused qkv projection
   run([&] {
+    if (int e = next_w(w.o_w)) return e;
     return gemm(ctx, dtype, lin.normed.ptr, w.qkv_w.ptr, lin.qkv.ptr, r, qkv_n, hs, qkv_n, 0, 0, 0,
                 1, false);
   });
@@ -169,17 +173,21 @@ int TextDecoder::layer(int li, int rows, hipEvent_t* ev) {
   });
   // 5. o projection + residual
   run([&] {
+    if (int e = next_w(w.gu_w)) return e;
     return gemm(ctx, dtype, lin.attn.ptr, w.o_w.ptr, lin.h.ptr, r, hs, qd, hs, 0, 0, 0, 1, true);
   });
   // 6. post-attention RMSNorm
   run([&] { return rms(l.pln, lin.norm2.ptr); });
   // 7. gate|up + SiLU.up
   run([&] {
+    if (int e = next_w(w.dp_w)) return e;
     return gemm(ctx, dtype, lin.norm2.ptr, w.gu_w.ptr, lin.act.ptr, r, 2 * (int64_t)inter, hs,
                 inter, 0, 0, 0, 1, false, QA_EPI_SILU_MUL);
   });
   // 8. down projection + residual
   run([&] {
+    if (li + 1 < layers)
+      if (int e = next_w(lin.L[(size_t)li + 1].qkv_w)) return e;
     return gemm(ctx, dtype, lin.act.ptr, w.dp_w.ptr, lin.h.ptr, r, hs, inter, hs, 0, 0, 0, 1,
                 true);
   });

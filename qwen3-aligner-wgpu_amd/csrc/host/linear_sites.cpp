@@ -195,26 +195,34 @@ int TextDecoderLinears::layer(int li, int rows, hipEvent_t* ev) {
   auto mark = [&](int i) {
     if (ev) (void)hipEventRecord(ev[i], s);
   };
+  // Each projection pulls the next one's weights toward the caches while it
+  // runs (the last down pulls the next layer's qkv weights).
+  auto next_w = [&](const Buffer& b) { return qa_prefetch_hint(ctx, b.ptr, b.bytes); };
   // 3. qkv:  normed x qkv_w^T  (src/decoder.rs:1321-1327)
   mark(0);
+  if (int rc = next_w(l.o_w)) return rc;
   if (int rc = gemm(ctx, dtype, normed.ptr, l.qkv_w.ptr, qkv.ptr, s_rows, qkv_n, hs, qkv_n, 0, 0,
                     0, 1, false))
     return rc;
   mark(1);
   // 8. o + residual:  h += attn_flat x o_w^T  (src/decoder.rs:1602-1608)
   mark(2);
+  if (int rc = next_w(l.gu_w)) return rc;
   if (int rc = gemm(ctx, dtype, attn.ptr, l.o_w.ptr, h.ptr, s_rows, hs, q_dim, hs, 0, 0, 0, 1,
                     true))
     return rc;
   mark(3);
   // 10. gate|up GEMM + silu_mul_split, one kernel  (src/decoder.rs:1628-1650)
   mark(4);
+  if (int rc = next_w(l.dp_w)) return rc;
   if (int rc = gemm(ctx, dtype, norm2.ptr, l.gu_w.ptr, act.ptr, s_rows, 2 * (int64_t)inter, hs,
                     inter, 0, 0, 0, 1, false, QA_EPI_SILU_MUL))
     return rc;
   mark(5);
   // down + residual:  h += act x dp_w^T  (src/decoder.rs:1652-1657)
   mark(6);
+  if (li + 1 < layers)
+    if (int rc = next_w(L[(size_t)li + 1].qkv_w)) return rc;
   if (int rc = gemm(ctx, dtype, act.ptr, l.dp_w.ptr, h.ptr, s_rows, hs, inter, hs, 0, 0, 0, 1,
                     true))
     return rc;

@@ -28,6 +28,10 @@ struct qa_ctx {
   float* ws = nullptr;  // split-K partials
   size_t ws_floats = 0;
   float* scratch = nullptr;  // this device's copy of `scratch` (qa_linear_noalloc)
+  // qa_prefetch_hint: bytes the projection after the next one reads; the next
+  // projection launch takes it over and clears it
+  const void* pf = nullptr;
+  size_t pf_bytes = 0;
 };
 
 // The allocation-free linear's split-K partials (qa_linear_noalloc): one
@@ -383,6 +387,12 @@ int launch_linear(qa_ctx* ctx, const qa_linear_desc* d, const qa::Plan& plan, fl
   p.accumulate = (d->flags & QA_ACCUMULATE) ? 1 : 0;
   p.bias_rows = (d->flags & QA_BIAS_ROWS) ? 1 : 0;
   p.group_m = plan.group_m;
+  if (ctx->pf && !plan.transb) {
+    p.pf = (const uint16_t*)ctx->pf;
+    p.pf_bytes = (int)std::min<size_t>(ctx->pf_bytes, (size_t)INT32_MAX & ~(size_t)127);
+  }
+  ctx->pf = nullptr;
+  ctx->pf_bytes = 0;
   const int batch = d->batch > 0 ? (int)d->batch : 1;
   if (plan.splits > 1 && batch > 1)
     return fail(QA_EUNSUPPORTED, "qa_linear: split-K with batch > 1");
@@ -533,6 +543,14 @@ int qa_linear_noalloc(qa_ctx* ctx, const qa_linear_desc* d) {
 
 size_t qa_linear_noalloc_scratch_floats(void) { return kScratchFloats; }
 
+int qa_prefetch_hint(qa_ctx* ctx, const void* ptr, size_t bytes) {
+  if (!ctx) return fail(QA_EINVAL, "qa_prefetch_hint: null context");
+  if (!ptr && bytes) return fail(QA_EINVAL, "qa_prefetch_hint: null pointer with %zu bytes", bytes);
+  ctx->pf = bytes ? ptr : nullptr;
+  ctx->pf_bytes = ptr ? bytes : 0;
+  return ok();
+}
+
 int qa_mlp_fused(qa_ctx* ctx, const qa_mlp_desc* d) {
   if (!ctx || !d) return fail(QA_EINVAL, "qa_mlp_fused: null argument");
   if (d->flags) return fail(QA_EINVAL, "qa_mlp_fused: flags must be 0");
@@ -566,6 +584,10 @@ int qa_mlp_fused(qa_ctx* ctx, const qa_mlp_desc* d) {
   down.batch = 1;
   if (int rc = validate(&gu)) return rc;
   if (int rc = validate(&down)) return rc;
+  // a caller's hint stays with the gate|up launch; otherwise it pulls the
+  // down projection's weights toward the caches
+  if (!ctx->pf)
+    if (int rc = qa_prefetch_hint(ctx, d->w_down, (size_t)(d->hidden * d->inter) * 2)) return rc;
   if (int rc = qa_linear(ctx, &gu)) return rc;
   return qa_linear(ctx, &down);
 }

@@ -168,16 +168,17 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
   return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g * kLog2e)) * u;
 }
 
-// Output stores are nontemporal: the next kernel reads the output from
-// whichever XCD its tile lands on, so keeping it in this XCD's L2 buys
-// nothing, and streaming it out shortens the end-of-kernel writeback
-// (measured 0.3-0.5 us less per launch for the 6-8 MB outputs at M = 1024).
+// Output stores are ordinary (temporal) stores.  Nontemporal ones shorten
+// the producing kernel's end by 0.3-0.5 us, but the next kernel, which reads
+// the output as its A operand or residual, then fetches it from HBM instead
+// of the memory-side cache: measured 3 us slower for the down projection
+// right after gate|up (18.7 against 14.9 us at M = 1024).
 template <int DT>
 __device__ __forceinline__ void store4(uint16_t* p, const float* v) {
   u32x2 w;
   w.x = Fmt<DT>::narrow(v[0]) | (Fmt<DT>::narrow(v[1]) << 16);
   w.y = Fmt<DT>::narrow(v[2]) | (Fmt<DT>::narrow(v[3]) << 16);
-  __builtin_nontemporal_store(w, reinterpret_cast<u32x2*>(p));
+  *reinterpret_cast<u32x2*>(p) = w;
 }
 
 template <int DT>
@@ -522,6 +523,31 @@ __global__ void __launch_bounds__(64 * (2 * WGN * KG + PW)) gemm_dma_kernel(cons
   // refills that buffer with stage it+S at once.
   static_assert(SPG % 2 == 0, "fragment slots alternate within a stage");
   const int kk0 = kg * SPG;
+
+  // Prefetch of the next kernel's operand (p.pf, a caller hint): each MMA
+  // wave loads one dword of PFI x 64 distinct 128-byte lines, so the lines
+  // travel HBM -> memory-side cache while this kernel computes, and the next
+  // kernel's first stages find them there instead of in HBM.  The loads are
+  // ordinary ones: with the nontemporal hint the next kernel measured no
+  // faster than with no prefetch at all.  The loaded values are only kept
+  // alive until the end of the kernel.  Where the MMA waves also issue the DMA (PW = 0), the
+  // loads sit in the same in-order vmcnt stream right after stage S-1: the
+  // waits for stages 1 .. S-1 leave them outstanding (+PFI), and the kernel
+  // prefetches only when every ring stage is issued up front (nk >= S).
+  constexpr int PFI = 2;
+  static_assert((S - 1) * LPS + PFI < 64, "vmcnt with the prefetch loads");
+  const bool pf_on = p.pf_bytes > 0 && z == 0 && mma_wave && (PW > 0 || nk >= S);
+  uint32_t pfv[PFI] = {};
+  auto prefetch = [&]() {
+    const __amdgpu_buffer_rsrc_t rsp = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(p.pf), (short)0, p.pf_bytes, 0x00020000);
+#pragma unroll
+    for (int i = 0; i < PFI; ++i) {
+      const uint64_t line = (uint64_t)((i * NMW + wave) * 64 + lane) * gridDim.x + blockIdx.x;
+      const uint32_t off = line * 128 < (uint64_t)p.pf_bytes ? (uint32_t)(line * 128) : OOB;
+      pfv[i] = __builtin_amdgcn_raw_buffer_load_b32(rsp, off, 0, 0);
+    }
+  };
   if (nk > 0 && !mma_wave) {
 #pragma unroll
     for (int s = 0; s < S; ++s)
@@ -550,6 +576,7 @@ __global__ void __launch_bounds__(64 * (2 * WGN * KG + PW)) gemm_dma_kernel(cons
         wait_vmcnt<0>();
     }
     exec_barrier();
+    if (pf_on) prefetch();
     read_frags(0, kk0, 0);
     for (int it = 0; it < nk; ++it) {
       const int buf = it % S;
@@ -561,10 +588,14 @@ __global__ void __launch_bounds__(64 * (2 * WGN * KG + PW)) gemm_dma_kernel(cons
       wait_lds();  // unconditional: both paths reach the last MFMAs with ready slots
       if (it + 1 < nk) {
         if (dma_wave) {
-          if (it + S - 1 < nk)
-            wait_vmcnt<(S - 2) * LPS>();
-          else
+          if (it + S - 1 < nk) {
+            if (PW == 0 && pf_on && it < S - 1)
+              wait_vmcnt<(S - 2) * LPS + PFI>();
+            else
+              wait_vmcnt<(S - 2) * LPS>();
+          } else {
             wait_vmcnt<0>();
+          }
         }
         exec_barrier();
         read_frags((it + 1) % S, kk0, 0);
@@ -652,6 +683,10 @@ __global__ void __launch_bounds__(64 * (2 * WGN * KG + PW)) gemm_dma_kernel(cons
       const float uu[4] = {u4.x, u4.y, u4.z, u4.w};
       epilogue4<DT, EPI>(p, C, m, n, v, uu);
     }
+  }
+  if (pf_on) {
+#pragma unroll
+    for (int i = 0; i < PFI; ++i) asm volatile("" ::"v"(pfv[i]));
   }
 }
 

@@ -82,6 +82,10 @@ struct GemmParams {
   int cv_c, cv_h, cv_w;  // input channels (multiple of 8, >= 64), height, width
   int cv_ho, cv_wo;      // output height, width
   int cv_tmajor;         // output rows ordered (b, wo, ho) instead of (b, ho, wo)
+  // Bytes the NEXT kernel will read (its weights), pulled into the memory-side
+  // cache while this one runs; pf_bytes = 0 for none (qa_prefetch_hint).
+  const uint16_t* pf;
+  int pf_bytes;
 };
 
 struct Plan {

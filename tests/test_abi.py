@@ -104,6 +104,8 @@ def test_calls_without_context_fail_cleanly(pkg):
     assert lib.qa_sync(None) == pkg.QA_EINVAL
     assert lib.qa_ctx_destroy(None) == pkg.QA_OK
     assert lib.qa_ctx_create(0, None) == pkg.QA_EINVAL
+    assert lib.qa_prefetch_hint(None, None, 0) == pkg.QA_EINVAL
+    assert "null context" in pkg.last_error()
     for fn, desc in ((lib.qa_rms_norm, pkg.RmsNormDesc()), (lib.qa_qk_norm_rope, pkg.QkRopeDesc()),
                      (lib.qa_attention_prefill, pkg.AttentionDesc()),
                      (lib.qa_layer_norm, pkg.LayerNormDesc()),
