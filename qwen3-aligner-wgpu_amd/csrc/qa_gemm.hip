@@ -168,17 +168,19 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
   return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g * kLog2e)) * u;
 }
 
-// Output stores are ordinary (temporal) stores.  Nontemporal ones shorten
-// the producing kernel's end by 0.3-0.5 us, but the next kernel, which reads
-// the output as its A operand or residual, then fetches it from HBM instead
-// of the memory-side cache: measured 3 us slower for the down projection
-// right after gate|up (18.7 against 14.9 us at M = 1024).
+// Output stores carry sc1 (device scope): the lines are written through the
+// XCD's L2 as they are stored, so the end-of-kernel release has no dirty
+// output to write back, and they stay cacheable for the next kernel, which
+// reads them as its A operand or residual.  Measured on the config-3 layer
+// sequence: 1.3% faster per step than plain stores.  Nontemporal stores
+// shorten the producer too, but then the consumer fetches its operand from
+// HBM: the down projection right after gate|up took 18.7 us against 14.9.
 template <int DT>
 __device__ __forceinline__ void store4(uint16_t* p, const float* v) {
   u32x2 w;
   w.x = Fmt<DT>::narrow(v[0]) | (Fmt<DT>::narrow(v[1]) << 16);
   w.y = Fmt<DT>::narrow(v[2]) | (Fmt<DT>::narrow(v[3]) << 16);
-  *reinterpret_cast<u32x2*>(p) = w;
+  asm volatile("global_store_dwordx2 %0, %1, off sc1" ::"v"(p), "v"(w) : "memory");
 }
 
 template <int DT>
