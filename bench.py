@@ -44,18 +44,21 @@ DEC = dict(layers=28, hidden=1024, q_dim=2048, kv_dim=1024, inter=3072, nqh=16, 
 PREFILL_ROWS = (1024, 4352)  # config 3's M; config 5's ~300 s prefill (~4.3 k tokens)
 ENC = dict(layers=18, d_model=896, ffn=3584, conv_k=128 * 9)
 COPY_CAL_BYTES = 512 << 20
-TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemm_decoder_config3_traffic.json")
+COUNTER_PROFILE = os.path.join(ROOT, "profiles", "gemm_sites_counters.json")
 
 
-def measured_traffic(site: str):
-    """HBM-side bytes per launch of a site's kernel, from the committed
-    FETCH_SIZE / WRITE_SIZE passes (scaled by the copy calibration), or None."""
+def measured_counters(site: str):
+    """From the committed rocprofv3 --pmc passes over `bench.py --site <site>`
+    (cold weights): L2 <-> fabric bytes per launch (FETCH_SIZE / WRITE_SIZE
+    scaled by the copy calibration), the kernel, and the MFMA-busy share
+    SQ_VALU_MFMA_BUSY_CYCLES / (1024 SIMDs x duration x 2.4 GHz); Nones when
+    the profile is missing."""
     try:
-        prof = json.load(open(TRAFFIC_PROFILE))
-        entry = prof["sites"][site]
-        return int(entry["traffic_bytes"]), entry["kernel"]
+        entry = json.load(open(COUNTER_PROFILE))["sites"][f"{site}/cold"]
+        return (int(entry["hbm_bytes"]), entry["kernel"], entry["mfma_busy_pct_duration_2p4GHz"],
+                entry["mfma_busy_pct_gui"])
     except (OSError, KeyError, ValueError):
-        return None, None
+        return None, None, None, None
 
 
 def log(*a):
@@ -355,6 +358,44 @@ def site_protocol(host, ctx, ss, warm_iters=200, cold_iters=280):
                          "layers, ms summed over per-launch events"}
 
 
+COLD_BYTES = 320 << 20  # weight copies a cold --site run cycles through: > the 256 MB MALL
+
+
+def site_descs(pkg, host, ctx, site, warm):
+    """One GEMM site for counter runs (rocprofv3 --pmc over bench.py --site):
+    config-3 sites (qkv, o, gu, down; q, k, v, gate, up unfused) at M = 1024,
+    config1 (x [256,1024] . W[3072,1024]^T) or config2_gu / config2_down (the
+    MLP block at M = 512).  warm: one weight matrix repeated (L2 / MALL
+    resident); cold: distinct copies of it totalling COLD_BYTES, cycled, so
+    every launch fetches its W from HBM.  Returns (descriptors, FLOPs per
+    launch)."""
+    h, q, kv, it = DEC["hidden"], DEC["q_dim"], DEC["kv_dim"], DEC["inter"]
+    sites = dict(dec_sites(False), **dec_sites(True))
+    if site == "config1":
+        m, n, k, fl, xk = 256, 3072, 1024, 0, None
+    elif site == "config2_gu":
+        m, n, k, fl, xk = 512, 2 * it, h, 2, None
+    elif site == "config2_down":
+        m, n, k, fl, xk = 512, h, it, 1, None
+    elif site in sites:
+        (n, k, fl), m = sites[site], 1024
+        xk = k
+    else:
+        raise SystemExit(f"bench.py: unknown --site {site}")
+    a = ctx.to_device(rmsnormed(host, 0, 31, (m, k), 0) if xk is not None
+                      else host.synth_normal(0, 32, (m, k), 0, 0.5))
+    nout = n // 2 if fl == 2 else n
+    c = ctx.to_device(host.synth_normal(0, 33, (m, nout)))
+    copies = 1 if warm else -(-COLD_BYTES // (n * k * 2))
+    w0 = host.synth_normal(0, 34, (n, k), 0, 0.02)
+    descs = []
+    for i in range(copies):
+        w = ctx.to_device(w0)  # identical values, distinct buffers: only the addresses rotate
+        flags = {0: 0, 1: pkg.ACCUMULATE, 2: pkg.EPI_SILU_MUL}[fl]
+        descs.append(pkg.linear_desc(pkg.F16, m, n, k, a, w, c, flags=flags, ldc=nout))
+    return descs, 2 * m * n * k
+
+
 def config1_protocol(pkg, host, ctx):
     """Config 1 (x [256,1024] . W[3072,1024]^T, HBM-bound): warm (one W) and
     cold (48 copies of W, 302 MB > the 256 MB MALL), with the algorithmic
@@ -602,19 +643,10 @@ def main():
 
     if args.site:
         with pkg.Context(0) as ctx:
-            if args.site == "config1":
-                m, n, k = 256, 3072, 1024
-                a = ctx.to_device(host.synth_normal(0, 11, (m, k)))
-                c = ctx.alloc(m * n * 2)
-                ws = [ctx.to_device(host.synth_normal(0, 12 if i == 0 else 1200 + i, (n, k), 0, 0.02))
-                      for i in range(1 if args.warm else 48)]
-                descs = [pkg.linear_desc(pkg.F16, m, n, k, a, w, c) for w in ws]
-            else:
-                unf = args.site in dec_sites(True) and args.site not in dec_sites(False)
-                ss = SiteSet(pkg, host, ctx, 1024, 1 if args.warm else DEC["layers"], unf)
-                descs = ss.descs[args.site]
+            descs, flops = site_descs(pkg, host, ctx, args.site, args.warm)
             ms = host.time_linears_each(ctx, descs, 0, args.launches)
-            print(json.dumps({"site": args.site, "warm": args.warm, "per_launch": dist(ms)}), flush=True)
+            print(json.dumps({"site": args.site, "warm": args.warm, "weight_sets": len(descs),
+                              "flops_per_launch": flops, "per_launch": dist(ms)}), flush=True)
         return
 
     if args.e2e_only:
@@ -708,7 +740,7 @@ def main():
         log(f"[bench] aligner forward 300 s: {e2e}")
     ctx.close()
 
-    traffic, traffic_kernel = measured_traffic("gu")
+    traffic, traffic_kernel, busy_pct, busy_pct_gui = measured_counters("gu")
     cpu = None
     if args.cpu_budget > 0:
         orc = entry.load_oracle()
@@ -749,7 +781,9 @@ def main():
             "frac": round(achieved / PEAK_F16_TFLOPS, 4),
             "traffic": traffic,
             "traffic_kernel": traffic_kernel,
-            "traffic_source": "profiles/gemm_decoder_config3_traffic.md" if traffic else None,
+            "mfma_busy_pct": busy_pct,
+            "mfma_busy_pct_over_gui_active": busy_pct_gui,
+            "counter_source": "profiles/gemm_sites_counters.md" if traffic else None,
         },
         "cpu_baseline": cpu,
         "detail": detail,
