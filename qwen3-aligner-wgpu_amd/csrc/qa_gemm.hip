@@ -893,9 +893,9 @@ hipError_t launch_epi(const Plan& plan, const GemmParams& p, int batch, hipStrea
       case TILE_64x64_P2:
         e = launch_dma<DT, 64, 64, 4, EPI, 2, 8, 0, 1, 2>(plan, p, batch, s);
         break;
-      case TILE_128x192: e = launch_dma<DT, 128, 192, 4, EPI, 2, 0>(plan, p, batch, s); break;
+      case TILE_128x192: e = launch_dma<DT, 128, 192, 3, EPI, 2, 0>(plan, p, batch, s); break;
       case TILE_256x256: e = launch_dma<DT, 256, 256, 2, EPI, 1, 0, 0, 4>(plan, p, batch, s); break;
-      default: e = launch_dma<DT, 128, 128, 5, EPI, 2, 8>(plan, p, batch, s); break;
+      default: e = launch_dma<DT, 128, 128, 3, EPI, 2, 8>(plan, p, batch, s); break;
     }
   }
   if (e != hipSuccess || plan.splits == 1) return e;
