@@ -309,7 +309,10 @@ int AudioEncoderLinears::set_inputs(int rows, const uint16_t* c, const uint16_t*
 }
 
 int AudioEncoderLinears::conv(int rows) {
-  // im2col GEMM + bias + GELU, token-major (src/audio_encoder.rs:416-447)
+  // im2col GEMM + bias + GELU, token-major (src/audio_encoder.rs:416-447);
+  // it pulls layer 0's qkv weights toward the caches
+  if (!L.empty())
+    if (int rc = qa_prefetch_hint(ctx, L[0].qkv.w.ptr, L[0].qkv.w.bytes)) return rc;
   return gemm(ctx, dtype, col.ptr, conv_w.w.ptr, conv_out.ptr, rows, conv_w.n_pad,
               conv_w.k_pad, d_model, 0, 0, 0, 1, false, QA_EPI_GELU, conv_w.b.ptr);
 }
@@ -321,26 +324,34 @@ int AudioEncoderLinears::layer(int li, int rows, hipEvent_t* ev) {
   auto mark = [&](int i) {
     if (ev) (void)hipEventRecord(ev[i], s);
   };
+  // each projection pulls the next one's weights toward the caches (the
+  // last fc2 pulls the next layer's qkv weights)
+  auto next_w = [&](const Linear& x) { return qa_prefetch_hint(ctx, x.w.ptr, x.w.bytes); };
   // qkv + bias  (src/audio_encoder_gpu.rs:1414-1419)
   mark(0);
+  if (int rc = next_w(l.o)) return rc;
   if (int rc = gemm(ctx, dtype, normed.ptr, l.qkv.w.ptr, qkv.ptr, rows, l.qkv.n_pad, d,
                     3 * d, 0, 0, 0, 1, false, 0, l.qkv.b.ptr))
     return rc;
   mark(1);
   // out_proj + bias, onto the residual  (src/audio_encoder_gpu.rs:1579-1581)
   mark(2);
+  if (int rc = next_w(l.fc1)) return rc;
   if (int rc = gemm(ctx, dtype, attn.ptr, l.o.w.ptr, h.ptr, rows, l.o.n_pad, d, d, 0, 0, 0, 1,
                     true, 0, l.o.b.ptr))
     return rc;
   mark(3);
   // fc1 + bias + GELU, one kernel  (src/audio_encoder_gpu.rs:1594-1602)
   mark(4);
+  if (int rc = next_w(l.fc2)) return rc;
   if (int rc = gemm(ctx, dtype, norm2.ptr, l.fc1.w.ptr, act.ptr, rows, l.fc1.n_pad, d, ffn, 0,
                     0, 0, 1, false, QA_EPI_GELU, l.fc1.b.ptr))
     return rc;
   mark(5);
   // fc2 + bias, onto the residual  (src/audio_encoder_gpu.rs:1603-1605)
   mark(6);
+  if (li + 1 < layers)
+    if (int rc = next_w(L[(size_t)li + 1].qkv)) return rc;
   if (int rc = gemm(ctx, dtype, act.ptr, l.fc2.w.ptr, h.ptr, rows, l.fc2.n_pad, ffn, d, 0, 0, 0,
                     1, true, 0, l.fc2.b.ptr))
     return rc;
