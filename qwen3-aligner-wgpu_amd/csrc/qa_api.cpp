@@ -282,10 +282,24 @@ void choose_group_m(qa::Plan& pl, int64_t span) {
 // the band height is chosen for that window.  For the same reason the
 // 128 x 256 tile comes first among equal costs: it gathers each input slab
 // for half as many n-tiles as 256 x 128.  Measured on the 300-chunk second
-// level (c = 480): 256 x 128 took 2.07 ms with the whole-range band (118
-// m-tiles, each slab re-fetched once per n-tile) and 1.50 ms with bands of
-// 8; 128 x 256 with the window's band takes 1.37-1.41 ms, and 256 x 256 (the
-// modelled choice there) 1.24-1.28 ms.
+// level (c = 480) with two k groups of MMA waves that issue their own DMA:
+// 256 x 128 took 2.07 ms with the whole-range band (118 m-tiles, each slab
+// re-fetched once per n-tile) and 1.50 ms with bands of 8; 128 x 256 with
+// the window's band 1.37-1.41 ms, and 256 x 256 1.13-1.28 ms.  With one k
+// group plus producer waves (the kernels now) 128 x 256 takes 1.08 ms and
+// 256 x 128 1.21 ms; the third level (62400 pixels) 264 us on 128 x 256
+// against 259 us on 256 x 256.  The per-stage costs of the CV loader, whose
+// address arithmetic per chunk and 9-tap gather cost more than the plain
+// loader's, are those kernel-trace times over the rounds and stages
+// (conv_stage_us).
+double conv_stage_us(int tile) {
+  switch (tile) {
+    case qa::TILE_128x256: return 1.09;
+    case qa::TILE_256x128: return 1.21;
+    case qa::TILE_256x256: return 2.27;
+    default: return 0.74;  // 128 x 128
+  }
+}
 qa::Plan plan_conv(int64_t M, int64_t N, int64_t K, bool gelu, int num_cus) {
   qa::Plan pl{};
   pl.epi = gelu ? qa::EPI_GELU : qa::EPI_PLAIN;
@@ -300,7 +314,7 @@ qa::Plan plan_conv(int64_t M, int64_t N, int64_t K, bool gelu, int num_cus) {
     const qa::TileShape ts = qa::tile_shape(tile);
     const int64_t tm = (M + ts.bm - 1) / ts.bm, tn = (N + ts.bn - 1) / ts.bn;
     const int64_t rounds = (tm * tn + num_cus - 1) / num_cus;
-    const double cost = (double)rounds * (kTileFixedUs + (double)pl.kchunk / 64.0 * stage_us(tile));
+    const double cost = (double)rounds * (kTileFixedUs + (double)pl.kchunk / 64.0 * conv_stage_us(tile));
     if (cost < best * 0.999) {
       best = cost;
       pl.tile = tile;
