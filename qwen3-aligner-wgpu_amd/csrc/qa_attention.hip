@@ -94,6 +94,17 @@ struct AFmt<QA_F16> {
   __device__ static __forceinline__ f32x2 unpack2(uint32_t h) {
     return __builtin_convertvector(__builtin_bit_cast(f16x2, h), f32x2);
   }
+  // (a, b) minus their 16-bit roundings h (packed: a's in the low half), as
+  // two 16-bit values.  Each difference is exact in f32 (a and h agree in
+  // their leading bits), so v_fma_mix_f32 (-h) * 1 + a, which reads h
+  // straight from its half of the packed word, gives the same bits as
+  // widening h and subtracting, in one instruction instead of two.
+  __device__ static __forceinline__ uint32_t residue2(uint32_t h, float a, float b) {
+    float d0, d1;
+    asm("v_fma_mix_f32 %0, -%1, 1.0, %2 op_sel_hi:[1,0,0]" : "=v"(d0) : "v"(h), "v"(a));
+    asm("v_fma_mix_f32 %0, -%1, 1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(d1) : "v"(h), "v"(b));
+    return pack2(d0, d1);
+  }
   // Probabilities are formed as p * 2^7; with the running max allowed to lag
   // the true one by up to 2^8 (kLazy) they stay <= 2^15, and the f16 range
   // keeps them normal down to p = 2^-21, so rounding them loses only relative
@@ -113,6 +124,10 @@ struct AFmt<QA_BF16> {
   }
   __device__ static __forceinline__ f32x2 unpack2(uint32_t h) {
     return (f32x2){__uint_as_float(h << 16), __uint_as_float(h & 0xffff0000u)};
+  }
+  __device__ static __forceinline__ uint32_t residue2(uint32_t h, float a, float b) {
+    const f32x2 hv = unpack2(h);
+    return pack2(a - hv[0], b - hv[1]);
   }
   static constexpr float kPBias = 0.f;
 };
@@ -362,10 +377,8 @@ __global__ void __launch_bounds__(NS * REP * 2 * 64) attention_kernel(const Attn
         pf[j][2 * half] = AFmt<DT>::pack2(pv[0], pv[1]);
         pf[j][2 * half + 1] = AFmt<DT>::pack2(pv[2], pv[3]);
         if constexpr (PS == 2) {  // the rounding residue as a second 16-bit term
-          const f32x2 h01 = AFmt<DT>::unpack2(pf[j][2 * half]);
-          const f32x2 h23 = AFmt<DT>::unpack2(pf[j][2 * half + 1]);
-          pl[j][2 * half] = AFmt<DT>::pack2(pv[0] - h01[0], pv[1] - h01[1]);
-          pl[j][2 * half + 1] = AFmt<DT>::pack2(pv[2] - h23[0], pv[3] - h23[1]);
+          pl[j][2 * half] = AFmt<DT>::residue2(pf[j][2 * half], pv[0], pv[1]);
+          pl[j][2 * half + 1] = AFmt<DT>::residue2(pf[j][2 * half + 1], pv[2], pv[3]);
         }
       }
     // this lane's half of the row sum; the halves are added once at the end
