@@ -110,3 +110,33 @@ def test_fused_mlp_with_and_without_a_caller_hint(ctx, pkg, orc, hint_buf):
     for b in (dx, dgu, dd):
         b.free()
     assert np.array_equal(res[0], res[1])
+
+
+@pytest.mark.parametrize("tile", [0, 5, 6, 7])
+def test_hint_with_a_batched_call(ctx, pkg, orc, hint_buf, tile):
+    """Batched problems (only the first problem's blocks prefetch): same bits
+    with and without a hint, each problem equal to its own single call."""
+    rng = np.random.default_rng(7100 + tile)
+    b, m, n, k = 3, 200, 256, 640
+    a = _h16(orc, rng.standard_normal((b, m, k)), 0)
+    w = _h16(orc, 0.02 * rng.standard_normal((b, n, k)), 0)
+    da, dw = ctx.to_device(a), ctx.to_device(w)
+    os.environ["QA_TILE"] = str(tile)
+    outs = []
+    try:
+        for hinted in (False, True):
+            dc = ctx.alloc(b * m * n * 2)
+            if hinted:
+                ctx.prefetch_hint(hint_buf)
+            ctx.linear(pkg.linear_desc(0, m, n, k, da, dw, dc, batch=b, bsa=m * k, bsb=n * k,
+                                       bsc=m * n))
+            outs.append(ctx.download(dc, (b, m, n)))
+            dc.free()
+    finally:
+        del os.environ["QA_TILE"]
+        da.free()
+        dw.free()
+    assert np.array_equal(outs[0], outs[1])
+    for i in range(b):
+        want = orc.linear(0, a[i], w[i], np.zeros((m, n), np.uint16), flags=orc.EXACT)
+        assert_parity(outs[1][i], want, orc, 0, ulp_tol=1)
