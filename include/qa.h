@@ -378,7 +378,8 @@ int qa_mel_filterbank(int n_mels, int n_fft, int sample_rate, float* out);
  * last zero (the chunking of encode, src/audio_encoder_gpu.rs:1079-1091).
  * samples and filterbank are device f32 buffers; needs n_samples >= 160
  * (at least one frame) and cs even.  Uses the context's workspace
- * (n_mels * frames floats), which grows only outside graph capture. */
+ * (n_mels * frames floats plus ~8 KB), which grows only outside graph
+ * capture. */
 typedef struct qa_mel_desc {
   uint32_t dtype;
   uint32_t flags; /* reserved, must be 0 */

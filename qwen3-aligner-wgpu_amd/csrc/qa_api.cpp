@@ -851,13 +851,18 @@ int qa_log_mel(qa_ctx* ctx, const qa_mel_desc* d) {
   p.n_mels = d->n_mels;
   p.cs = d->cs;
   p.n_chunks = (int)((p.frames + d->cs - 1) / d->cs);
-  p.nblocks = (int)((p.frames + 15) / 16);
-  const size_t floats = (size_t)p.n_mels * (size_t)p.frames + (size_t)p.nblocks;
+  p.nblocks = (int)((p.frames + qa::kMelFramesPerBlock - 1) / qa::kMelFramesPerBlock);
+  // workspace: logmel, block maxima, then (from a 64-float boundary) the
+  // twiddle table and the filters' supports
+  const size_t tw_at = ((size_t)p.n_mels * (size_t)p.frames + (size_t)p.nblocks + 63) & ~(size_t)63;
+  const size_t floats = tw_at + 800 * 2 + 2 * (size_t)p.n_mels;
   if (int rc = ensure_workspace(ctx, floats)) return rc;
   p.x = d->samples;
   p.filt = d->filterbank;
   p.logmel = ctx->ws;
   p.bmax = ctx->ws + (size_t)p.n_mels * (size_t)p.frames;
+  p.tw = reinterpret_cast<double*>(ctx->ws + tw_at);
+  p.sup = reinterpret_cast<int32_t*>(ctx->ws + tw_at + 800 * 2);
   p.out = (uint16_t*)d->out;
   const hipError_t e = qa::launch_log_mel((int)d->dtype, p, ctx->stream);
   return e == hipSuccess ? ok() : hip_fail(e, "qa_log_mel launch");

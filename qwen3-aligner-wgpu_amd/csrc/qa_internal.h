@@ -172,11 +172,14 @@ struct Conv1Params {
 hipError_t launch_conv1(int dtype, const Conv1Params& p, hipStream_t stream);
 
 // Log-mel front end (qa_mel.hip).
+constexpr int kMelFramesPerBlock = 9;  // frames per block of mel_log_kernel
 struct MelParams {
   const float* x;      // samples [n]
   const float* filt;   // [n_mels][201]
   float* logmel;       // workspace [n_mels][frames]
   float* bmax;         // workspace [nblocks]
+  double* tw;          // workspace [400][2]: cos, sin of 2 pi j / 400
+  int32_t* sup;        // workspace [n_mels][2]: each filter's nonzero bins [lo, hi)
   uint16_t* out;       // [n_chunks][n_mels][cs]
   int64_t n, frames;
   int n_mels, cs, n_chunks, nblocks;
