@@ -928,7 +928,7 @@ int qa_timestamp_head(qa_ctx* ctx, const qa_head_desc* d) {
     return fail(QA_EINVAL, "qa_timestamp_head: dtype %u is neither QA_F16 nor QA_BF16", d->dtype);
   if (d->flags) return fail(QA_EINVAL, "qa_timestamp_head: flags must be 0");
   if (d->rows < 0 || d->n <= 0 || d->n > kI32 || d->labels <= 0 || d->labels > kI32 ||
-      d->h_rows < 0 || d->ldh < d->n || (d->rows + 63) / 64 > 65535)
+      d->h_rows < 0 || d->ldh < d->n || (d->rows + 15) / 16 > 65535)
     return fail(QA_EINVAL, "qa_timestamp_head: bad shape");
   if (!d->positions || !d->h || !d->norm_w || !d->score || !d->logits || !d->classes)
     return fail(QA_EINVAL, "qa_timestamp_head: null pointer");

@@ -56,84 +56,118 @@ __global__ void __launch_bounds__(256) head_norm_kernel(const HeadParams p) {
     p.normed[r * p.n + j] = ok ? widen<DT>(x[j]) * p.w[j] * inv : 0.f;
 }
 
-// logits[r][l] = sum_j normed[r][j] score[l][j] in f32, j in order: 64 rows x
-// 64 labels per block, k in slabs of 64 through LDS stored k-major, so a
-// thread reads its 4 rows and its 4 labels of one k as two 16-byte loads and
-// does 16 FMAs with them.  The next slab is loaded into registers while the
-// current one multiplies.  VEC: rows of n floats are 16-byte aligned
-// (n % 4 == 0 and an aligned score), so each thread fetches 16 consecutive k
-// of one row / label as four 16-byte loads.
-template <bool VEC>
+// logits[r][l] = sum_j normed[r][j] score[l][j] in f32, j in order (each sum
+// is one chain of FMAs, as the reference's f32 linear).  A block takes 16 PR
+// rows x 64 labels, k in slabs of 64 through LDS stored k-major; a thread
+// owns PR rows and 4 labels: per k, PR broadcast reads of its rows' values,
+// one 16-byte read of its labels' and 4 PR FMAs.  The next slab is loaded
+// into registers while the current one multiplies.  The launch picks the
+// smallest PR whose grid fits one block per CU, so each SIMD runs one wave
+// and the score matrix (20 MB at 5000 labels) is read by as few row blocks
+// as that allows: at 240 rows x 5000 labels, PR = 5 and 3 x 79 blocks.
+// VEC: rows of n floats are 16-byte aligned (n % 4 == 0 and aligned
+// pointers), so the loaders fetch 16-byte chunks.
+template <bool VEC, int PR>
 __global__ void __launch_bounds__(256) head_logits_kernel(const HeadParams p) {
   typedef float f32x4 __attribute__((ext_vector_type(4)));
-  constexpr int KS = 64;
-  __shared__ __attribute__((aligned(16))) float as[KS][64 + 4], bs[KS][64 + 4];
+  constexpr int KS = 64, RB = 16 * PR, LB = 64;
+  constexpr int AC = RB * KS / 4 / 256;  // A chunks (4 k of one row) per thread per slab
+  __shared__ __attribute__((aligned(16))) float as[KS][RB];
+  __shared__ __attribute__((aligned(16))) float bs[KS][LB];
   const int t = threadIdx.x;
-  const int64_t r0 = (int64_t)blockIdx.y * 64, l0 = (int64_t)blockIdx.x * 64;
-  const int tr = t >> 4, tl = t & 15;  // rows 4 tr .. 4 tr + 3, labels 4 tl .. 4 tl + 3
-  // loader: row / label ld = t / 4, k k0 + 16 (t % 4) .. + 15
-  const int ld = t >> 2, lk = (t & 3) * 16;
-  const bool arow = r0 + ld < p.rows, brow = l0 + ld < p.labels;
-  const float* ap = p.normed + (arow ? (r0 + ld) * p.n : 0);
-  const float* bp = p.score + (brow ? (l0 + ld) * p.n : 0);
-  float ra[16], rb[16];
+  const int64_t r0 = (int64_t)blockIdx.y * RB, l0 = (int64_t)blockIdx.x * LB;
+  const int tr = t >> 4, tl = t & 15;  // rows tr + 16 u (u < PR), labels 4 tl .. 4 tl + 3
+  // loaders: A chunk c = t + 256 j: row c % RB, k 4 (c / RB) .. + 3;
+  // B label t % 64, k 16 (t / 64) .. + 15
+  const int bl = t & 63, bk = (t >> 6) * 16;
+  const bool brow = l0 + bl < p.labels;
+  const float* bp = p.score + (brow ? (l0 + bl) * p.n : 0);
+  float ra[AC][4], rb[16];
   auto load = [&](int k0) {
+#pragma unroll
+    for (int j = 0; j < AC; ++j) {
+      const int c = t + 256 * j, ar = c % RB, k = k0 + (c / RB) * 4;
+      const bool arow = r0 + ar < p.rows;
+      const float* ap = p.normed + (arow ? (r0 + ar) * p.n : 0);
+      if constexpr (VEC) {
+        const f32x4 va = (arow && k < p.n) ? *reinterpret_cast<const f32x4*>(ap + k) : f32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ra[j][e] = va[e];
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ra[j][e] = (arow && k + e < p.n) ? ap[k + e] : 0.f;
+      }
+    }
     if constexpr (VEC) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int k = k0 + lk + 4 * q;
-        const bool in = k < p.n;  // n % 4 == 0: a chunk is all in or all out
-        const f32x4 va = (arow && in) ? *reinterpret_cast<const f32x4*>(ap + k) : f32x4{0, 0, 0, 0};
-        const f32x4 vb = (brow && in) ? *reinterpret_cast<const f32x4*>(bp + k) : f32x4{0, 0, 0, 0};
+        const int kb = k0 + bk + 4 * q;  // n % 4 == 0: a chunk is all in or all out
+        const f32x4 vb = (brow && kb < p.n) ? *reinterpret_cast<const f32x4*>(bp + kb) : f32x4{0, 0, 0, 0};
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          ra[4 * q + e] = va[e];
-          rb[4 * q + e] = vb[e];
-        }
+        for (int e = 0; e < 4; ++e) rb[4 * q + e] = vb[e];
       }
     } else {
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int k = k0 + lk + e;
-        ra[e] = (arow && k < p.n) ? ap[k] : 0.f;
-        rb[e] = (brow && k < p.n) ? bp[k] : 0.f;
-      }
+      for (int e = 0; e < 16; ++e) rb[e] = (brow && k0 + bk + e < p.n) ? bp[k0 + bk + e] : 0.f;
     }
   };
-  float acc[4][4];
+  float acc[PR][4];
 #pragma unroll
-  for (int u = 0; u < 4; ++u)
+  for (int u = 0; u < PR; ++u)
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc[u][i] = 0.f;
   load(0);
   for (int k0 = 0; k0 < p.n; k0 += KS) {
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      as[lk + e][ld] = ra[e];
-      bs[lk + e][ld] = rb[e];
+    for (int j = 0; j < AC; ++j) {
+      const int c = t + 256 * j;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) as[(c / RB) * 4 + e][c % RB] = ra[j][e];
     }
+#pragma unroll
+    for (int e = 0; e < 16; ++e) bs[bk + e][bl] = rb[e];
     __syncthreads();
     if (k0 + KS < p.n) load(k0 + KS);
-#pragma unroll 8
+#pragma unroll 4
     for (int kk = 0; kk < KS; ++kk) {
-      const f32x4 a4 = *reinterpret_cast<const f32x4*>(&as[kk][4 * tr]);
       const f32x4 b4 = *reinterpret_cast<const f32x4*>(&bs[kk][4 * tl]);
 #pragma unroll
-      for (int u = 0; u < 4; ++u)
+      for (int u = 0; u < PR; ++u) {
+        const float a = as[kk][tr + 16 * u];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[u][i] += a4[u] * b4[i];
+        for (int i = 0; i < 4; ++i) acc[u][i] += a * b4[i];
+      }
     }
     __syncthreads();
   }
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int64_t r = r0 + 4 * tr + u;
+  for (int u = 0; u < PR; ++u) {
+    const int64_t r = r0 + tr + 16 * u;
     if (r >= p.rows) continue;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int64_t l = l0 + 4 * tl + i;
       if (l < p.labels) p.logits[r * p.labels + l] = acc[u][i];
     }
+  }
+}
+
+template <bool VEC>
+void launch_logits(const HeadParams& p, hipStream_t s) {
+  constexpr int kCUs = 256;
+  const int64_t lb = (p.labels + 63) / 64;
+  int pr = 1;
+  while (pr < 8 && lb * ((p.rows + 16 * pr - 1) / (16 * pr)) > kCUs) ++pr;
+  const dim3 g((unsigned)lb, (unsigned)((p.rows + 16 * pr - 1) / (16 * pr))), t(256);
+  switch (pr) {
+    case 1: hipLaunchKernelGGL((head_logits_kernel<VEC, 1>), g, t, 0, s, p); break;
+    case 2: hipLaunchKernelGGL((head_logits_kernel<VEC, 2>), g, t, 0, s, p); break;
+    case 3: hipLaunchKernelGGL((head_logits_kernel<VEC, 3>), g, t, 0, s, p); break;
+    case 4: hipLaunchKernelGGL((head_logits_kernel<VEC, 4>), g, t, 0, s, p); break;
+    case 5: hipLaunchKernelGGL((head_logits_kernel<VEC, 5>), g, t, 0, s, p); break;
+    case 6: hipLaunchKernelGGL((head_logits_kernel<VEC, 6>), g, t, 0, s, p); break;
+    case 7: hipLaunchKernelGGL((head_logits_kernel<VEC, 7>), g, t, 0, s, p); break;
+    default: hipLaunchKernelGGL((head_logits_kernel<VEC, 8>), g, t, 0, s, p); break;
   }
 }
 
@@ -146,11 +180,18 @@ __global__ void __launch_bounds__(256) head_argmax_kernel(const HeadParams p) {
   const float* row = p.logits + r * p.labels;
   float bv = -INFINITY;
   int bi = p.labels;
-  for (int l = lane; l < p.labels; l += 64)
-    if (row[l] > bv) {
-      bv = row[l];
-      bi = l;
-    }
+  // 8 loads in flight per lane, then its labels in increasing order
+  for (int64_t l0 = lane; l0 < p.labels; l0 += 512) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = l0 + 64 * u < p.labels ? row[l0 + 64 * u] : -INFINITY;
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (v[u] > bv) {
+        bv = v[u];
+        bi = (int)(l0 + 64 * u);
+      }
+  }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
     const float ov = __shfl_xor(bv, o, 64);
@@ -176,12 +217,11 @@ hipError_t launch_timestamp_head(int dtype, const HeadParams& p, hipStream_t s) 
     hipLaunchKernelGGL(head_norm_kernel<QA_BF16>, rows4, dim3(256), 0, s, p);
   else
     hipLaunchKernelGGL(head_norm_kernel<QA_F16>, rows4, dim3(256), 0, s, p);
-  const dim3 lg((unsigned)((p.labels + 63) / 64), (unsigned)((p.rows + 63) / 64));
   if (p.n % 4 == 0 && (reinterpret_cast<uintptr_t>(p.score) & 15) == 0 &&
       (reinterpret_cast<uintptr_t>(p.normed) & 15) == 0)
-    hipLaunchKernelGGL(head_logits_kernel<true>, lg, dim3(256), 0, s, p);
+    launch_logits<true>(p, s);
   else
-    hipLaunchKernelGGL(head_logits_kernel<false>, lg, dim3(256), 0, s, p);
+    launch_logits<false>(p, s);
   hipLaunchKernelGGL(head_argmax_kernel, rows4, dim3(256), 0, s, p);
   return hipGetLastError();
 }
