@@ -166,7 +166,10 @@ __global__ void __launch_bounds__(NS * REP * 2 * 64) attention_kernel(const Attn
   static_assert(KI * GW * 4 == KB && VI * GW * 8 == HD, "DMA row coverage");
   __shared__ __attribute__((aligned(1024))) unsigned char smem[NS * 2 * (KTILE + VTILE)];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  // the wave index as a scalar, so the LDS targets of the DMA (M0) and the
+  // ring slots are computed once per wave, not per lane
+  const int wave = tid >> 6;
   const int split = wave / GW, wg = wave % GW;
   const int hh = wg / 2, rg = wg & 1;
   const int fr = lane & 31, fh = lane >> 5;
@@ -197,17 +200,38 @@ __global__ void __launch_bounds__(NS * REP * 2 * 64) attention_kernel(const Attn
       const_cast<uint16_t*>(kbase), (short)0, (int)(p.cap * HD * 2), 0x00020000);
   const __amdgpu_buffer_rsrc_t rsv = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(vbase), (short)0, (int)(p.cap * HD * 2), 0x00020000);
+  // Per-lane byte offsets of this wave's chunks at key block 0.  K
+  // instruction j fills key rows 4 (GW j + wg) + lane / 16 and V instruction j
+  // d rows 8 (GW j + wg) + lane / 8; with GW = 4 the K chunk swizzle (row & 15)
+  // and for any GW the V chunk swizzle ((d >> 1) & 7) are the same for every
+  // j, so instruction j's offset is the lane's offset at j = 0 plus a
+  // wave-uniform amount: one add per instruction.  K rows at or past cap lie
+  // past the buffer's num_records and read as zeros; a V column at or past cap
+  // would not (it lies inside the next d row), so those lanes get OOB.
+  // (The lane offsets are recomputed at each refill, a few instructions, from
+  // a copy of the lane index the compiler cannot hoist: kept live across the
+  // loop they would push the kernel past its register budget.)
+  auto lane_opaque = [&]() {
+    int l = lane;
+    asm volatile("" : "+v"(l));
+    return l;
+  };
   auto issue_k = [&](int it) {
     unsigned char* sk = kslot(it);
     const int kb = split + NS * it;
+    const int l = lane_opaque(), rk = wg * 4 + (l >> 4);
+    const uint32_t koff0 = (uint32_t)((rk * HD + (((l & 15) ^ kswz(rk)) << 3)) * 2);
 #pragma unroll
     for (int j = 0; j < KI; ++j) {
-      const int ins = j * GW + wg;            // 16 instructions, 4 key rows each
-      const int r = ins * 4 + (lane >> 4);    // key row within the tile
-      const int pc = lane & 15;
-      const int64_t key = (int64_t)kb * KB + r;
-      const uint32_t off =
-          key < p.cap ? (uint32_t)((key * HD + ((pc ^ kswz(r)) << 3)) * 2) : OOB;
+      const int ins = j * GW + wg;
+      uint32_t off;
+      if constexpr (GW * 4 % 16 == 0) {
+        off = koff0 + (uint32_t)(((int64_t)kb * KB + 4 * GW * j) * HD * 2);
+      } else {
+        const int r = ins * 4 + (l >> 4);  // key row within the tile
+        const int64_t key = (int64_t)kb * KB + r;
+        off = key < p.cap ? (uint32_t)((key * HD + (((l & 15) ^ kswz(r)) << 3)) * 2) : OOB;
+      }
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rsk, (QA_LDS void*)(sk + ins * 1024), 16, off, 0,
                                                0, 0);
     }
@@ -215,13 +239,15 @@ __global__ void __launch_bounds__(NS * REP * 2 * 64) attention_kernel(const Attn
   auto issue_v = [&](int it) {
     unsigned char* sv = vslot(it);
     const int kb = split + NS * it;
+    const int l = lane_opaque(), dv = wg * 8 + (l >> 3);
+    const int vc = ((l & 7) ^ vswz(dv)) << 3;
+    const uint32_t voff0 = (uint32_t)(((int64_t)dv * p.cap + vc) * 2);
+    const bool vin = (int64_t)kb * KB + vc < p.cap;
 #pragma unroll
     for (int j = 0; j < VI; ++j) {
-      const int ins = j * GW + wg;            // 16 instructions, 8 d rows each
-      const int d = ins * 8 + (lane >> 3);
-      const int pc = lane & 7;
-      const int64_t col = (int64_t)kb * KB + ((pc ^ vswz(d)) << 3);
-      const uint32_t off = col < p.cap ? (uint32_t)(((int64_t)d * p.cap + col) * 2) : OOB;
+      const int ins = j * GW + wg;
+      const uint32_t off =
+          vin ? voff0 + (uint32_t)(((int64_t)8 * GW * j * p.cap + (int64_t)kb * KB) * 2) : OOB;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rsv, (QA_LDS void*)(sv + ins * 1024), 16, off, 0,
                                                0, 0);
     }
