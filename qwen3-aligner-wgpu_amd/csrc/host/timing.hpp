@@ -13,11 +13,15 @@ namespace qa_host {
 
 inline int timing_status(hipError_t e) { return e == hipSuccess ? QA_OK : QA_EDEVICE; }
 
-// Runs `step` warmup + steps times; optional graph capture of one step.
+// Runs `step` warmup + steps times; optional graph capture of one step.  A
+// captured step is preceded by at least one eager one, whatever `warmup`
+// says: the first call of a step sizes the context's workspace, which
+// cannot grow under capture.
 template <class Step>
 int time_steps(qa_ctx* ctx, int warmup, int steps, int use_graph, Step&& step, double* ms,
                double* wall_ms = nullptr) {
   hipStream_t s = (hipStream_t)qa_ctx_stream(ctx);
+  if (use_graph && warmup < 1) warmup = 1;
   for (int i = 0; i < warmup; ++i)
     if (int rc = step()) return rc;
   if (int rc = qa_sync(ctx)) return rc;

@@ -143,3 +143,28 @@ def test_decoder_two_layers_chain(ctx, pkg, orc, dtype, rows):
     ulp = 2.0 ** -10 if dtype == 0 else 2.0 ** -7
     assert mae <= 1e-3 * (1 if dtype == 0 else 8), mae
     assert rel_rms <= ulp, rel_rms
+
+
+def test_graph_timing_without_warmup(pkg, orc):
+    """The host's step timer captures one step into a hipGraph after at least
+    one eager step even with warmup = 0: the first call of a step sizes the
+    context's workspace, which cannot grow under capture (a fresh context, so
+    nothing is sized yet)."""
+    from qwen3_aligner_wgpu_amd import host
+    rng = np.random.default_rng(11)
+    rows = 96
+    ws = _weights(rng, orc, 0, 1)
+    h0 = orc.h16_from_f32(rng.standard_normal((rows, HID)).astype(np.float32), 0)
+    cos, sin = rope_tables(rows, HD, 0, dtype=0)
+    with pkg.Context(0) as fresh:
+        dec = host.TextDecoder(fresh, 0, 1, rows)
+        try:
+            w = ws[0]
+            dec.load_layer(0, w["q"], w["k"], w["v"], w["o"], w["gate"], w["up"], w["down"],
+                           w["iln"], w["pln"], w["qn"], w["kn"])
+            dec.set_rope(cos, sin)
+            dec.set_hidden(h0)
+            ms, wall = dec.time(rows, 0, 2, use_graph=True)
+        finally:
+            dec.close()
+    assert 0 < ms < 1e3 and 0 < wall < 1e3, (ms, wall)
