@@ -424,6 +424,7 @@ __global__ void __launch_bounds__(64 * (2 * WGN * KG + PW)) gemm_dma_kernel(cons
   uint32_t aoff[AJ], woff[BJ];
   int akc[AJ], wkc[BJ];  // k offset (elements) of the fetched chunk
   int cpix[AJ], cih[AJ], ciw[AJ];  // CV: image's first pixel, input row / column of tap (0, 0)
+  int cg[AJ], cic[AJ];             // CV: tap and channel of the lane's chunk in the next plane issued
 #pragma unroll
   for (int j = 0; j < AJ; ++j) {
     const int r = (j * NW + dwave) * 8 + lrow;
@@ -437,6 +438,8 @@ __global__ void __launch_bounds__(64 * (2 * WGN * KG + PW)) gemm_dma_kernel(cons
       cpix[j] = b * p.cv_h * p.cv_w;
       cih[j] = m < p.M ? 2 * ho - 1 : INT32_MIN / 2;  // rows >= M never in range
       ciw[j] = 2 * wo - 1;
+      cg[j] = (kbeg + akc[j]) / p.cv_c;
+      cic[j] = kbeg + akc[j] - cg[j] * p.cv_c;
     }
   }
 #pragma unroll
@@ -457,7 +460,12 @@ __global__ void __launch_bounds__(64 * (2 * WGN * KG + PW)) gemm_dma_kernel(cons
       uint32_t off;
       if constexpr (CV) {
         const int k = k0 + akc[j];
-        const int g = k / p.cv_c, ic = k - g * p.cv_c;  // tap g = 3 kh + kw
+        const int g = cg[j], ic = cic[j];  // tap g = 3 kh + kw
+        cic[j] += BK;  // the next plane: 64 channels on (c >= 64: at most one wrap)
+        if (cic[j] >= p.cv_c) {
+          cic[j] -= p.cv_c;
+          ++cg[j];
+        }
         const int kh = (g * 11) >> 5, kw = g - 3 * kh;   // g / 3 for g < 9
         const int ih = cih[j] + kh, iw = ciw[j] + kw;
         const bool ok = k < kend && (unsigned)ih < (unsigned)p.cv_h && (unsigned)iw < (unsigned)p.cv_w;
