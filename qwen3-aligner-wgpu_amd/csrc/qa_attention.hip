@@ -166,10 +166,7 @@ __global__ void __launch_bounds__(NS * REP * 2 * 64) attention_kernel(const Attn
   static_assert(KI * GW * 4 == KB && VI * GW * 8 == HD, "DMA row coverage");
   __shared__ __attribute__((aligned(1024))) unsigned char smem[NS * 2 * (KTILE + VTILE)];
 
-  const int tid = threadIdx.x, lane = tid & 63;
-  // the wave index as a scalar, so the LDS targets of the DMA (M0) and the
-  // ring slots are computed once per wave, not per lane
-  const int wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int split = wave / GW, wg = wave % GW;
   const int hh = wg / 2, rg = wg & 1;
   const int fr = lane & 31, fh = lane >> 5;

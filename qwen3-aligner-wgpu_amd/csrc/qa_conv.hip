@@ -8,10 +8,12 @@
 // products run on the matrix cores as a K = 16 product (taps 9..15 zero): a
 // wave multiplies 32 output pixels by the weights of 32 output channels per
 // v_mfma_f32_32x32x16, every product of two 16-bit values exact in f32.  What
-// is left on the VALU per output is the bias add, the erf GELU (a reciprocal,
-// an exponential and ~15 more operations) and the rounding: ~20 slots, which
-// over the 300-chunk stem (461 M outputs) is ~0.24 ms of the 256 CUs' VALU
-// issue, against ~30 slots with the taps on the VALU as well.
+// is left on the VALU per output is the bias add, the erf GELU (a reciprocal
+// and an exponential, both at a quarter of the full rate, and ~15 more
+// operations) and the rounding: over the 300-chunk stem (461 M outputs) about
+// 0.3 ms of the 256 CUs' VALU issue at 2.4 GHz, against ~30 more slots per
+// output with the taps on the VALU as well (0.43 ms measured before, 0.35
+// after).
 //
 // A block takes 128 output pixels (32 per wave) x every output channel: the
 // weights sit in LDS as 16 taps per channel (zero-padded), the bias as f32;
