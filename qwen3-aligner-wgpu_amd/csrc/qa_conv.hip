@@ -11,7 +11,7 @@
 // is left on the VALU per output is the bias add, the erf GELU (a reciprocal
 // and an exponential, both at a quarter of the full rate, and ~15 more
 // operations) and the rounding: over the 300-chunk stem (461 M outputs) about
-// 0.3 ms of the 256 CUs' VALU issue at 2.4 GHz, against ~30 more slots per
+// 0.3 ms of the 256 CUs' VALU issue at 2.4 GHz, against ~30 slots per
 // output with the taps on the VALU as well (0.43 ms measured before, 0.35
 // after).
 //
