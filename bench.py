@@ -17,8 +17,10 @@ are resident in HBM before timing starts.
 `value` is TFLOP/s over the whole step (2*M*N*K per GEMM, host clock around
 exactly --steps steps with the stream synchronized on both sides).
 `roofline` prices the dominant kernel (the gate|up GEMM, 40% of the FLOPs)
-against the published MI355X dense FP16 peak, from its average launch
-duration measured with HIP events on the launching stream.  `cpu_baseline`
+against the published MI355X dense FP16 peak, from its average kernel
+duration over eager passes of the same layer sequence, each launch stamping
+start and end HIP events from its own dispatch (qa_time_next_launch, on the
+launching stream).  `cpu_baseline`
 times the oracle (the C restatement of the reference CPU path) on a bounded
 sample of the same workload on this host's cores.  `detail` carries the
 other BASELINE configs (1, 2, 4) as kernel-level figures.

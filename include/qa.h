@@ -178,6 +178,16 @@ size_t qa_linear_noalloc_scratch_floats(void);
  * for layer loops that stream a model's weights once per step
  * (src/decoder.rs:1321-1657 runs qkv, o, gate|up, down per layer). */
 int qa_prefetch_hint(qa_ctx* ctx, const void* ptr, size_t bytes);
+/* Timing hook: the NEXT projection launched on this context (as for
+ * qa_prefetch_hint) records the start and the end of its GEMM kernel into
+ * these HIP events (hipEvent_t, created by the caller; either may be null),
+ * stamped by the kernel's dispatch itself (hipExtLaunchKernel) rather than by
+ * event packets queued between kernels, which add a gap of their own.  A
+ * split-K reduce kernel after the GEMM is not inside the pair.  The launch
+ * that takes the events over clears them; not for launches under graph
+ * capture.  No counterpart in the reference; for per-kernel timing in
+ * harnesses (bench.py's per-site figures). */
+int qa_time_next_launch(qa_ctx* ctx, void* start_event, void* stop_event);
 /* Launch the MLP block (see qa_mlp_desc). */
 int qa_mlp_fused(qa_ctx* ctx, const qa_mlp_desc* desc);
 

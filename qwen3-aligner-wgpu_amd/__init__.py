@@ -277,6 +277,7 @@ EXPORTS = (
     "qa_ctx_create", "qa_ctx_destroy", "qa_ctx_stream", "qa_alloc", "qa_free",
     "qa_upload", "qa_download", "qa_sync", "qa_linear", "qa_linear_validate",
     "qa_linear_noalloc", "qa_linear_noalloc_scratch_floats", "qa_prefetch_hint",
+    "qa_time_next_launch",
     "qa_mlp_fused", "qa_rms_norm", "qa_qk_norm_rope", "qa_attention_prefill",
     "qa_layer_norm", "qa_window_attention", "qa_add_position_table", "qa_conv2d_3x3s2",
     "qa_mel_filterbank", "qa_log_mel", "qa_rope_tables", "qa_embed_scatter", "qa_timestamp_head",
@@ -309,6 +310,7 @@ def lib() -> ctypes.CDLL:
         L.qa_linear.argtypes = [vp, ctypes.POINTER(LinearDesc)]
         L.qa_linear_noalloc.argtypes = [vp, ctypes.POINTER(LinearDesc)]
         L.qa_prefetch_hint.argtypes = [vp, vp, sz]
+        L.qa_time_next_launch.argtypes = [vp, vp, vp]
         L.qa_linear_validate.argtypes = [ctypes.POINTER(LinearDesc)]
         L.qa_mlp_fused.argtypes = [vp, ctypes.POINTER(MlpDesc)]
         L.qa_rms_norm.argtypes = [vp, ctypes.POINTER(RmsNormDesc)]

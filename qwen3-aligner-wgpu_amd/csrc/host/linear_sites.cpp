@@ -192,41 +192,38 @@ int TextDecoderLinears::layer(int li, int rows, hipEvent_t* ev) {
   const Layer& l = L[(size_t)li];
   hipStream_t s = (hipStream_t)qa_ctx_stream(ctx);
   const int64_t s_rows = rows, hs = hidden, qkv_n = q_dim + 2 * kv_dim;
-  auto mark = [&](int i) {
-    if (ev) (void)hipEventRecord(ev[i], s);
+  // per-site kernel times: the site's GEMM dispatch stamps ev[2 i], ev[2 i + 1]
+  auto stamp = [&](int site) {
+    return ev ? qa_time_next_launch(ctx, ev[2 * site], ev[2 * site + 1]) : QA_OK;
   };
   // Each projection pulls the next one's weights toward the caches while it
   // runs (the last down pulls the next layer's qkv weights).
   auto next_w = [&](const Buffer& b) { return qa_prefetch_hint(ctx, b.ptr, b.bytes); };
   // 3. qkv:  normed x qkv_w^T  (src/decoder.rs:1321-1327)
-  mark(0);
+  if (int rc = stamp(0)) return rc;
   if (int rc = next_w(l.o_w)) return rc;
   if (int rc = gemm(ctx, dtype, normed.ptr, l.qkv_w.ptr, qkv.ptr, s_rows, qkv_n, hs, qkv_n, 0, 0,
                     0, 1, false))
     return rc;
-  mark(1);
   // 8. o + residual:  h += attn_flat x o_w^T  (src/decoder.rs:1602-1608)
-  mark(2);
+  if (int rc = stamp(1)) return rc;
   if (int rc = next_w(l.gu_w)) return rc;
   if (int rc = gemm(ctx, dtype, attn.ptr, l.o_w.ptr, h.ptr, s_rows, hs, q_dim, hs, 0, 0, 0, 1,
                     true))
     return rc;
-  mark(3);
   // 10. gate|up GEMM + silu_mul_split, one kernel  (src/decoder.rs:1628-1650)
-  mark(4);
+  if (int rc = stamp(2)) return rc;
   if (int rc = next_w(l.dp_w)) return rc;
   if (int rc = gemm(ctx, dtype, norm2.ptr, l.gu_w.ptr, act.ptr, s_rows, 2 * (int64_t)inter, hs,
                     inter, 0, 0, 0, 1, false, QA_EPI_SILU_MUL))
     return rc;
-  mark(5);
   // down + residual:  h += act x dp_w^T  (src/decoder.rs:1652-1657)
-  mark(6);
+  if (int rc = stamp(3)) return rc;
   if (li + 1 < layers)
     if (int rc = next_w(L[(size_t)li + 1].qkv_w)) return rc;
   if (int rc = gemm(ctx, dtype, act.ptr, l.dp_w.ptr, h.ptr, s_rows, hs, inter, hs, 0, 0, 0, 1,
                     true))
     return rc;
-  mark(7);
   return QA_OK;
 }
 
@@ -321,41 +318,38 @@ int AudioEncoderLinears::layer(int li, int rows, hipEvent_t* ev) {
   const Layer& l = L[(size_t)li];
   hipStream_t s = (hipStream_t)qa_ctx_stream(ctx);
   const int64_t d = d_model;
-  auto mark = [&](int i) {
-    if (ev) (void)hipEventRecord(ev[i], s);
+  // per-site kernel times: the site's GEMM dispatch stamps ev[2 i], ev[2 i + 1]
+  auto stamp = [&](int site) {
+    return ev ? qa_time_next_launch(ctx, ev[2 * site], ev[2 * site + 1]) : QA_OK;
   };
   // each projection pulls the next one's weights toward the caches (the
   // last fc2 pulls the next layer's qkv weights)
   auto next_w = [&](const Linear& x) { return qa_prefetch_hint(ctx, x.w.ptr, x.w.bytes); };
   // qkv + bias  (src/audio_encoder_gpu.rs:1414-1419)
-  mark(0);
+  if (int rc = stamp(0)) return rc;
   if (int rc = next_w(l.o)) return rc;
   if (int rc = gemm(ctx, dtype, normed.ptr, l.qkv.w.ptr, qkv.ptr, rows, l.qkv.n_pad, d,
                     3 * d, 0, 0, 0, 1, false, 0, l.qkv.b.ptr))
     return rc;
-  mark(1);
   // out_proj + bias, onto the residual  (src/audio_encoder_gpu.rs:1579-1581)
-  mark(2);
+  if (int rc = stamp(1)) return rc;
   if (int rc = next_w(l.fc1)) return rc;
   if (int rc = gemm(ctx, dtype, attn.ptr, l.o.w.ptr, h.ptr, rows, l.o.n_pad, d, d, 0, 0, 0, 1,
                     true, 0, l.o.b.ptr))
     return rc;
-  mark(3);
   // fc1 + bias + GELU, one kernel  (src/audio_encoder_gpu.rs:1594-1602)
-  mark(4);
+  if (int rc = stamp(2)) return rc;
   if (int rc = next_w(l.fc2)) return rc;
   if (int rc = gemm(ctx, dtype, norm2.ptr, l.fc1.w.ptr, act.ptr, rows, l.fc1.n_pad, d, ffn, 0,
                     0, 0, 1, false, QA_EPI_GELU, l.fc1.b.ptr))
     return rc;
-  mark(5);
   // fc2 + bias, onto the residual  (src/audio_encoder_gpu.rs:1603-1605)
-  mark(6);
+  if (int rc = stamp(3)) return rc;
   if (li + 1 < layers)
     if (int rc = next_w(L[(size_t)li + 1].qkv)) return rc;
   if (int rc = gemm(ctx, dtype, act.ptr, l.fc2.w.ptr, h.ptr, rows, l.fc2.n_pad, ffn, d, 0, 0, 0,
                     1, true, 0, l.fc2.b.ptr))
     return rc;
-  mark(7);
   return QA_OK;
 }
 
@@ -549,15 +543,13 @@ int qah_encoder_time(qah_encoder* e, int rows, int warmup, int steps, int use_gr
 int qah_encoder_profile_sites(qah_encoder* e, int rows, int steps, double* site_ms) {
   if (!e || !site_ms || steps <= 0) return QA_EINVAL;
   AudioEncoderLinears& E = *e->e;
-  hipStream_t s = (hipStream_t)qa_ctx_stream(E.ctx);
   std::vector<hipEvent_t> ev((size_t)E.layers * 8 + 2);
   for (auto& x : ev) (void)hipEventCreate(&x);
   double acc[5] = {0, 0, 0, 0, 0};
   int rc = QA_OK;
   for (int st = 0; st < steps && rc == QA_OK; ++st) {
-    (void)hipEventRecord(ev[(size_t)E.layers * 8], s);
-    rc = E.conv(rows);
-    (void)hipEventRecord(ev[(size_t)E.layers * 8 + 1], s);
+    rc = qa_time_next_launch(E.ctx, ev[(size_t)E.layers * 8], ev[(size_t)E.layers * 8 + 1]);
+    if (rc == QA_OK) rc = E.conv(rows);
     for (int li = 0; li < E.layers && rc == QA_OK; ++li) rc = E.layer(li, rows, &ev[(size_t)li * 8]);
     if (rc == QA_OK) rc = qa_sync(E.ctx);
     float t = 0.f;

@@ -75,8 +75,9 @@ int qah_decoder_read(qah_decoder* d, int which, int rows, uint16_t* host);
  * replays one captured hipGraph per step. */
 int qah_decoder_time(qah_decoder* d, int rows, int warmup, int steps, int use_graph,
                      double* ms_per_step, double* wall_ms_per_step);
-/* Per-site average kernel duration (ms) over `steps` passes, each launch
- * bracketed by its own pair of HIP events: site_ms[0..3] = qkv, o, gu, down. */
+/* Per-site average kernel duration (ms) over `steps` eager passes, each GEMM
+ * kernel stamping its own start / end events at dispatch (qa_time_next_launch):
+ * site_ms[0..3] = qkv, o, gu, down. */
 int qah_decoder_profile_sites(qah_decoder* d, int rows, int steps, double* site_ms);
 void qah_decoder_destroy(qah_decoder* d);
 
@@ -105,7 +106,8 @@ int qah_encoder_forward_linears(qah_encoder* e, int rows);
 int qah_encoder_read(qah_encoder* e, int which, int rows, uint16_t* host);
 int qah_encoder_time(qah_encoder* e, int rows, int warmup, int steps, int use_graph,
                      double* ms_per_step, double* wall_ms_per_step);
-/* site_ms[0..4] = conv, qkv, o, fc1, fc2 */
+/* The same per GEMM site of the tower (qa_time_next_launch stamps):
+ * site_ms[0..4] = conv, qkv, o, fc1, fc2 */
 int qah_encoder_profile_sites(qah_encoder* e, int rows, int steps, double* site_ms);
 void qah_encoder_destroy(qah_encoder* e);
 

@@ -32,6 +32,8 @@ struct qa_ctx {
   // projection launch takes it over and clears it
   const void* pf = nullptr;
   size_t pf_bytes = 0;
+  // qa_time_next_launch: events the next projection's GEMM kernel stamps
+  hipEvent_t t0 = nullptr, t1 = nullptr;
 };
 
 // The allocation-free linear's split-K partials (qa_linear_noalloc): one
@@ -407,10 +409,12 @@ int launch_linear(qa_ctx* ctx, const qa_linear_desc* d, const qa::Plan& plan, fl
   }
   ctx->pf = nullptr;
   ctx->pf_bytes = 0;
+  const hipEvent_t t0 = ctx->t0, t1 = ctx->t1;
+  ctx->t0 = ctx->t1 = nullptr;
   const int batch = d->batch > 0 ? (int)d->batch : 1;
   if (plan.splits > 1 && batch > 1)
     return fail(QA_EUNSUPPORTED, "qa_linear: split-K with batch > 1");
-  const hipError_t e = qa::launch_gemm((int)d->dtype, plan, p, batch, ctx->stream);
+  const hipError_t e = qa::launch_gemm((int)d->dtype, plan, p, batch, ctx->stream, t0, t1);
   return e == hipSuccess ? ok() : hip_fail(e, "qa_linear launch");
 }
 
@@ -562,6 +566,13 @@ int qa_prefetch_hint(qa_ctx* ctx, const void* ptr, size_t bytes) {
   if (!ptr && bytes) return fail(QA_EINVAL, "qa_prefetch_hint: null pointer with %zu bytes", bytes);
   ctx->pf = bytes ? ptr : nullptr;
   ctx->pf_bytes = ptr ? bytes : 0;
+  return ok();
+}
+
+int qa_time_next_launch(qa_ctx* ctx, void* start_event, void* stop_event) {
+  if (!ctx) return fail(QA_EINVAL, "qa_time_next_launch: null context");
+  ctx->t0 = (hipEvent_t)start_event;
+  ctx->t1 = (hipEvent_t)stop_event;
   return ok();
 }
 

@@ -42,6 +42,8 @@
 // gemm_reg_kernel is the W-as-[K, N] form (the reference's `transb` conv
 // operand, src/shaders.rs:1936-1944): register-staged loads that transpose the
 // operand into the same K-contiguous LDS layout.
+#include <hip/hip_ext.h>
+
 #include "qa_internal.h"
 
 namespace qa {
@@ -847,20 +849,35 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(const GemmParams p) 
   epilogue4<DT, EPI>(p, p.c, m, n, v, uu);
 }
 
-template <int DT, int BM, int BN, int S, int EPI, int KG, int PW, int CV = 0, int WGN = 2,
-          int PL = 1>
-hipError_t launch_dma(const Plan& plan, const GemmParams& p, int batch, hipStream_t s) {
-  const unsigned units = (unsigned)(plan.tiles_m * plan.tiles_n * plan.splits);
-  hipLaunchKernelGGL((gemm_dma_kernel<DT, BM, BN, S, EPI, KG, PW, CV, WGN, PL>),
-                     dim3(units, (unsigned)batch), dim3(64 * (2 * WGN * KG + PW)), 0, s, p);
+// Launch timing events (launch_gemm's t0 / t1), null for none.
+struct Stamps {
+  hipEvent_t t0, t1;
+};
+
+template <class K>
+hipError_t launch_kernel(K k, dim3 grid, dim3 block, hipStream_t s, const Stamps& ts,
+                         const GemmParams& p) {
+  if (ts.t0 || ts.t1)
+    hipExtLaunchKernelGGL(k, grid, block, 0, s, ts.t0, ts.t1, 0, p);
+  else
+    hipLaunchKernelGGL(k, grid, block, 0, s, p);
   return hipGetLastError();
 }
 
-template <int DT, int EPI>
-hipError_t launch_reg(const Plan& plan, const GemmParams& p, int batch, hipStream_t s) {
+template <int DT, int BM, int BN, int S, int EPI, int KG, int PW, int CV = 0, int WGN = 2,
+          int PL = 1>
+hipError_t launch_dma(const Plan& plan, const GemmParams& p, int batch, hipStream_t s,
+                      const Stamps& ts) {
   const unsigned units = (unsigned)(plan.tiles_m * plan.tiles_n * plan.splits);
-  hipLaunchKernelGGL((gemm_reg_kernel<DT, EPI>), dim3(units, (unsigned)batch), dim3(NT), 0, s, p);
-  return hipGetLastError();
+  return launch_kernel(gemm_dma_kernel<DT, BM, BN, S, EPI, KG, PW, CV, WGN, PL>,
+                       dim3(units, (unsigned)batch), dim3(64 * (2 * WGN * KG + PW)), s, ts, p);
+}
+
+template <int DT, int EPI>
+hipError_t launch_reg(const Plan& plan, const GemmParams& p, int batch, hipStream_t s,
+                      const Stamps& ts) {
+  const unsigned units = (unsigned)(plan.tiles_m * plan.tiles_n * plan.splits);
+  return launch_kernel(gemm_reg_kernel<DT, EPI>, dim3(units, (unsigned)batch), dim3(NT), s, ts, p);
 }
 
 template <int DT, int EPI>
@@ -873,35 +890,36 @@ hipError_t launch_reduce(const GemmParams& p, hipStream_t s) {
 }
 
 template <int DT, int EPI>
-hipError_t launch_epi(const Plan& plan, const GemmParams& p, int batch, hipStream_t s) {
+hipError_t launch_epi(const Plan& plan, const GemmParams& p, int batch, hipStream_t s,
+                      const Stamps& ts) {
   hipError_t e;
   if (plan.conv) {  // implicit-GEMM convolution (qa_conv2d_3x3s2)
     if constexpr (EPI == EPI_SILU) return hipErrorInvalidValue;  // never planned
     else if (plan.tile == TILE_256x128)
-      e = launch_dma<DT, 256, 128, 3, EPI, 1, 4, 1>(plan, p, batch, s);
+      e = launch_dma<DT, 256, 128, 3, EPI, 1, 4, 1>(plan, p, batch, s, ts);
     else if (plan.tile == TILE_128x256)
-      e = launch_dma<DT, 128, 256, 3, EPI, 1, 4, 1>(plan, p, batch, s);
+      e = launch_dma<DT, 128, 256, 3, EPI, 1, 4, 1>(plan, p, batch, s, ts);
     else if (plan.tile == TILE_256x256)
-      e = launch_dma<DT, 256, 256, 2, EPI, 1, 0, 1, 4>(plan, p, batch, s);
+      e = launch_dma<DT, 256, 256, 2, EPI, 1, 0, 1, 4>(plan, p, batch, s, ts);
     else
-      e = launch_dma<DT, 128, 128, 3, EPI, 1, 8, 1>(plan, p, batch, s);
+      e = launch_dma<DT, 128, 128, 3, EPI, 1, 8, 1>(plan, p, batch, s, ts);
   } else if (plan.transb) {
     if constexpr (EPI == EPI_SILU) return hipErrorInvalidValue;  // rejected by validation
-    else e = launch_reg<DT, EPI>(plan, p, batch, s);
+    else e = launch_reg<DT, EPI>(plan, p, batch, s, ts);
   } else {
     switch (plan.tile) {
       // (one k group of MMA waves plus 4 producer waves: 2-10% faster than two
       // k groups that issue their own DMA, on the prefill and tower shapes)
-      case TILE_256x128: e = launch_dma<DT, 256, 128, 3, EPI, 1, 4>(plan, p, batch, s); break;
-      case TILE_128x256: e = launch_dma<DT, 128, 256, 3, EPI, 1, 4>(plan, p, batch, s); break;
-      case TILE_64x128: e = launch_dma<DT, 64, 128, 4, EPI, 2, 8>(plan, p, batch, s); break;
+      case TILE_256x128: e = launch_dma<DT, 256, 128, 3, EPI, 1, 4>(plan, p, batch, s, ts); break;
+      case TILE_128x256: e = launch_dma<DT, 128, 256, 3, EPI, 1, 4>(plan, p, batch, s, ts); break;
+      case TILE_64x128: e = launch_dma<DT, 64, 128, 4, EPI, 2, 8>(plan, p, batch, s, ts); break;
       // 64x64: waves of 32 (m) x 64 (n) and an 8-deep ring (less LDS read per
       // FLOP than 32 x 32 waves with 6 stages): 7-8% faster at M = N = 1024 on
       // repeated launches over L2-resident operands, ~1% in the decoder-layer
       // sequence, where each launch starts on cold weights.
-      case TILE_64x64: e = launch_dma<DT, 64, 64, 8, EPI, 2, 8, 0, 1>(plan, p, batch, s); break;
+      case TILE_64x64: e = launch_dma<DT, 64, 64, 8, EPI, 2, 8, 0, 1>(plan, p, batch, s, ts); break;
       case TILE_64x64_P2:
-        e = launch_dma<DT, 64, 64, 4, EPI, 2, 8, 0, 1, 2>(plan, p, batch, s);
+        e = launch_dma<DT, 64, 64, 4, EPI, 2, 8, 0, 1, 2>(plan, p, batch, s, ts);
         break;
       // 128x192 and 128x128: one k group of 2 x 2 MMA waves that run the
       // whole 64-deep stage, plus producer waves that only issue the DMA.
@@ -909,9 +927,9 @@ hipError_t launch_epi(const Plan& plan, const GemmParams& p, int batch, hipStrea
       // or share it with producers, the stage's L2 -> LDS stream is faster
       // and the epilogue has no k-group sum: config 3 -3 / -1.3%, the
       // 4352-token prefill -3%, the 300 s forward -2% (same box).
-      case TILE_128x192: e = launch_dma<DT, 128, 192, 3, EPI, 1, 4>(plan, p, batch, s); break;
-      case TILE_256x256: e = launch_dma<DT, 256, 256, 2, EPI, 1, 0, 0, 4>(plan, p, batch, s); break;
-      default: e = launch_dma<DT, 128, 128, 3, EPI, 1, 8>(plan, p, batch, s); break;
+      case TILE_128x192: e = launch_dma<DT, 128, 192, 3, EPI, 1, 4>(plan, p, batch, s, ts); break;
+      case TILE_256x256: e = launch_dma<DT, 256, 256, 2, EPI, 1, 0, 0, 4>(plan, p, batch, s, ts); break;
+      default: e = launch_dma<DT, 128, 128, 3, EPI, 1, 8>(plan, p, batch, s, ts); break;
     }
   }
   if (e != hipSuccess || plan.splits == 1) return e;
@@ -919,20 +937,22 @@ hipError_t launch_epi(const Plan& plan, const GemmParams& p, int batch, hipStrea
 }
 
 template <int DT>
-hipError_t launch_dt(const Plan& plan, const GemmParams& p, int batch, hipStream_t s) {
+hipError_t launch_dt(const Plan& plan, const GemmParams& p, int batch, hipStream_t s,
+                     const Stamps& ts) {
   switch (plan.epi) {
-    case EPI_GELU: return launch_epi<DT, EPI_GELU>(plan, p, batch, s);
-    case EPI_SILU: return launch_epi<DT, EPI_SILU>(plan, p, batch, s);
-    default: return launch_epi<DT, EPI_PLAIN>(plan, p, batch, s);
+    case EPI_GELU: return launch_epi<DT, EPI_GELU>(plan, p, batch, s, ts);
+    case EPI_SILU: return launch_epi<DT, EPI_SILU>(plan, p, batch, s, ts);
+    default: return launch_epi<DT, EPI_PLAIN>(plan, p, batch, s, ts);
   }
 }
 
 }  // namespace
 
 hipError_t launch_gemm(int dtype, const Plan& plan, const GemmParams& p, int batch,
-                       hipStream_t stream) {
-  if (dtype == QA_BF16) return launch_dt<QA_BF16>(plan, p, batch, stream);
-  return launch_dt<QA_F16>(plan, p, batch, stream);
+                       hipStream_t stream, hipEvent_t t0, hipEvent_t t1) {
+  const Stamps ts{t0, t1};
+  if (dtype == QA_BF16) return launch_dt<QA_BF16>(plan, p, batch, stream, ts);
+  return launch_dt<QA_F16>(plan, p, batch, stream, ts);
 }
 
 }  // namespace qa

@@ -98,9 +98,11 @@ struct Plan {
   bool conv = false;  // A is an implicit convolution operand (GemmParams::cv_*)
 };
 
-// Launch one planned GEMM on `stream` (grid = tiles*splits x batch).
+// Launch one planned GEMM on `stream` (grid = tiles*splits x batch).  With
+// t0 / t1 set, the GEMM kernel's dispatch records its start / end into them
+// (hipExtLaunchKernel).
 hipError_t launch_gemm(int dtype, const Plan& plan, const GemmParams& p, int batch,
-                       hipStream_t stream);
+                       hipStream_t stream, hipEvent_t t0 = nullptr, hipEvent_t t1 = nullptr);
 
 // qa_rms_norm (qa_decoder_ops.hip).
 struct RmsParams {

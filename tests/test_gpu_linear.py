@@ -315,3 +315,50 @@ def test_accumulate_with_zero_a_keeps_c(ctx, pkg, orc):
     c0 = _h16(orc, rng.standard_normal((m, n)), 0)
     got = _run(ctx, pkg, 0, a, w, c0, flags=pkg.ACCUMULATE)
     assert np.array_equal(got, c0)
+
+
+def test_time_next_launch_stamps_the_kernel(ctx, pkg, orc):
+    """qa_time_next_launch: the next GEMM's dispatch records its start and end
+    into the caller's HIP events (a positive interval below the whole
+    launch-to-sync time), the result is the same as without the events, and
+    the launch after it records nothing (the events are taken over once)."""
+    import ctypes
+    import time
+
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+    hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p,
+                                        ctypes.c_void_p]
+    hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+    ev = [ctypes.c_void_p(), ctypes.c_void_p()]
+    for e in ev:
+        assert hip.hipEventCreate(ctypes.byref(e)) == 0
+    rng = np.random.default_rng(12)
+    m, n, k = 1024, 1024, 2048
+    a = _h16(orc, rng.standard_normal((m, k)), 0)
+    w = _h16(orc, 0.02 * rng.standard_normal((n, k)), 0)
+    c0 = np.zeros((m, n), np.uint16)
+    plain = _run(ctx, pkg, 0, a, w, c0)
+    da, dw, dc = ctx.to_device(a), ctx.to_device(w), ctx.to_device(c0)
+    desc = pkg.linear_desc(0, m, n, k, da, dw, dc)
+    try:
+        ctx.sync()
+        t = time.perf_counter()
+        pkg.check(pkg.lib().qa_time_next_launch(ctx.handle, ev[0], ev[1]))
+        ctx.linear(desc)
+        ctx.sync()
+        wall_ms = (time.perf_counter() - t) * 1e3
+        ms = ctypes.c_float()
+        assert hip.hipEventElapsedTime(ctypes.byref(ms), ev[0], ev[1]) == 0
+        assert 0.0 < ms.value < wall_ms, (ms.value, wall_ms)
+        stamped = ctx.download(dc, c0.shape)
+        ctx.linear(desc)  # no events: the hook was cleared by the launch above
+        ctx.sync()
+        again = ctx.download(dc, c0.shape)
+    finally:
+        for b in (da, dw, dc):
+            b.free()
+        for e in ev:
+            hip.hipEventDestroy(e)
+    assert np.array_equal(stamped, plain)
+    assert np.array_equal(again, plain)
