@@ -190,7 +190,6 @@ int TextDecoderLinears::set_inputs(int rows, const uint16_t* n1, const uint16_t*
 
 int TextDecoderLinears::layer(int li, int rows, hipEvent_t* ev) {
   const Layer& l = L[(size_t)li];
-  hipStream_t s = (hipStream_t)qa_ctx_stream(ctx);
   const int64_t s_rows = rows, hs = hidden, qkv_n = q_dim + 2 * kv_dim;
   // per-site kernel times: the site's GEMM dispatch stamps ev[2 i], ev[2 i + 1]
   auto stamp = [&](int site) {
@@ -316,7 +315,6 @@ int AudioEncoderLinears::conv(int rows) {
 
 int AudioEncoderLinears::layer(int li, int rows, hipEvent_t* ev) {
   const Layer& l = L[(size_t)li];
-  hipStream_t s = (hipStream_t)qa_ctx_stream(ctx);
   const int64_t d = d_model;
   // per-site kernel times: the site's GEMM dispatch stamps ev[2 i], ev[2 i + 1]
   auto stamp = [&](int site) {
