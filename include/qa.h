@@ -184,9 +184,10 @@ int qa_prefetch_hint(qa_ctx* ctx, const void* ptr, size_t bytes);
  * stamped by the kernel's dispatch itself (hipExtLaunchKernel) rather than by
  * event packets queued between kernels, which add a gap of their own.  A
  * split-K reduce kernel after the GEMM is not inside the pair.  The launch
- * that takes the events over clears them; not for launches under graph
- * capture.  No counterpart in the reference; for per-kernel timing in
- * harnesses (bench.py's per-site figures). */
+ * that takes the events over clears them; under stream capture that launch
+ * fails with QA_EINVAL (a captured dispatch does not stamp them on replay).
+ * No counterpart in the reference; for per-kernel timing in harnesses
+ * (bench.py's per-site figures). */
 int qa_time_next_launch(qa_ctx* ctx, void* start_event, void* stop_event);
 /* Launch the MLP block (see qa_mlp_desc). */
 int qa_mlp_fused(qa_ctx* ctx, const qa_mlp_desc* desc);

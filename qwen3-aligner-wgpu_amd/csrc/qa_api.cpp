@@ -411,6 +411,15 @@ int launch_linear(qa_ctx* ctx, const qa_linear_desc* d, const qa::Plan& plan, fl
   ctx->pf_bytes = 0;
   const hipEvent_t t0 = ctx->t0, t1 = ctx->t1;
   ctx->t0 = ctx->t1 = nullptr;
+  if (t0 || t1) {
+    // a captured dispatch does not stamp them on replay (the graph keeps an
+    // event node that reads back as garbage)
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(ctx->stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+      return fail(QA_EINVAL,
+                  "qa_linear: timing events from qa_time_next_launch cannot be recorded under "
+                  "stream capture");
+  }
   const int batch = d->batch > 0 ? (int)d->batch : 1;
   if (plan.splits > 1 && batch > 1)
     return fail(QA_EUNSUPPORTED, "qa_linear: split-K with batch > 1");
