@@ -8,9 +8,10 @@
 //  * v_mfma_f32_32x32x16_{f16,bf16}.  The operands are swapped relative to
 //    C = A.W^T: the MFMA's A operand is a 32-row slice of W (32 output columns
 //    n), its B operand a 32-row slice of A (32 tokens m), so each lane's
-//    accumulators hold ONE token and runs of 4 consecutive columns: the
-//    epilogue stores 8-byte packs and finds a gate column and its up column
-//    in the same lane.
+//    accumulators hold ONE token and runs of 4 consecutive columns.  The
+//    LDS-staged epilogue stores 8-byte packs; it finds a gate column and its
+//    up column (the first and second half of a SiLU tile's W rows, held by
+//    different waves) in one row of the parked tile.
 //  * Both operands are K-contiguous in HBM, the natural MFMA operand layout:
 //    no transposition anywhere.  Tiles stream HBM -> LDS with
 //    buffer_load_dwordx4 ... lds (direct to LDS, no VGPR staging) into an
@@ -251,24 +252,15 @@ __device__ __forceinline__ int w_row(const GemmParams& p, int tn, int r) {
   }
 }
 
-// Wave-local 32-column subtile fn -> subtile index within the W tile.
-template <int BN, int FN, int EPI>
-__device__ __forceinline__ int n_subtile(int wn, int fn) {
-  if constexpr (EPI == EPI_SILU) {
-    constexpr int H = FN / 2;
-    return (fn / H) * (BN / 64) + wn * H + (fn % H);
-  } else {
-    return wn * FN + fn;
-  }
-}
-
-// Shared tail: epilogue (splits == 1) or f32 partials (splits > 1).
-// Lane (fr, fh) of MFMA tile (fm, fn) holds token m = .. + fr and columns
-// 8g + 4fh + {0,1,2,3} of the tile's 32-column subtile fn.
+// gemm_reg_kernel's tail: epilogue (splits == 1) or f32 partials (splits >
+// 1) straight from the accumulators.  Lane (fr, fh) of MFMA tile (fm, fn)
+// holds token m = .. + fr and columns 8g + 4fh + {0,1,2,3} of the wave's
+// 32-column subtile wn FN + fn.  No SiLU.up (QA_TRANSB refuses it).
 template <int DT, int BM, int BN, int EPI, int FM, int FN, int WTM>
 __device__ __forceinline__ void finish_tile(const GemmParams& p, f32x16 (&acc)[FM][FN], uint16_t* C,
                                             int tm, int tn, int split, int wm, int wn, int fr,
                                             int fh) {
+  static_assert(EPI != EPI_SILU, "QA_TRANSB takes no SiLU.up");
   const int m0 = tm * BM;
   if (p.splits > 1) {
     f32x4* ws = reinterpret_cast<f32x4*>(p.ws);
@@ -281,9 +273,8 @@ __device__ __forceinline__ void finish_tile(const GemmParams& p, f32x16 (&acc)[F
       for (int fn = 0; fn < FN; ++fn) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const int r = n_subtile<BN, FN, EPI>(wn, fn) * 32 + 8 * g + 4 * fh;
-          const int n = w_row<BN, EPI>(p, tn, r);
-          if (n < 0) continue;
+          const int n = tn * BN + (wn * FN + fn) * 32 + 8 * g + 4 * fh;
+          if (n >= p.N) continue;
           const f32x4 v = {acc[fm][fn][4 * g], acc[fm][fn][4 * g + 1], acc[fm][fn][4 * g + 2],
                            acc[fm][fn][4 * g + 3]};
           ws[(rowbase + n) >> 2] = v;
@@ -296,33 +287,15 @@ __device__ __forceinline__ void finish_tile(const GemmParams& p, f32x16 (&acc)[F
   for (int fm = 0; fm < FM; ++fm) {
     const int m = m0 + wm * WTM + fm * 32 + fr;
     if (m >= p.M) continue;
-    if constexpr (EPI == EPI_SILU) {
-      constexpr int H = FN / 2;
-      const int nout = p.N >> 1;
 #pragma unroll
-      for (int fn = 0; fn < H; ++fn) {
+    for (int fn = 0; fn < FN; ++fn) {
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int n = tn * (BN / 2) + n_subtile<BN, FN, EPI>(wn, fn) * 32 + 8 * g + 4 * fh;
-          if (n >= nout) continue;
-          const float v[4] = {acc[fm][fn][4 * g], acc[fm][fn][4 * g + 1], acc[fm][fn][4 * g + 2],
-                              acc[fm][fn][4 * g + 3]};
-          const float u[4] = {acc[fm][fn + H][4 * g], acc[fm][fn + H][4 * g + 1],
-                              acc[fm][fn + H][4 * g + 2], acc[fm][fn + H][4 * g + 3]};
-          epilogue4<DT, EPI>(p, C, m, n, v, u);
-        }
-      }
-    } else {
-#pragma unroll
-      for (int fn = 0; fn < FN; ++fn) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int n = tn * BN + n_subtile<BN, FN, EPI>(wn, fn) * 32 + 8 * g + 4 * fh;
-          if (n >= p.N) continue;
-          const float v[4] = {acc[fm][fn][4 * g], acc[fm][fn][4 * g + 1], acc[fm][fn][4 * g + 2],
-                              acc[fm][fn][4 * g + 3]};
-          epilogue4<DT, EPI>(p, C, m, n, v, nullptr);
-        }
+      for (int g = 0; g < 4; ++g) {
+        const int n = tn * BN + (wn * FN + fn) * 32 + 8 * g + 4 * fh;
+        if (n >= p.N) continue;
+        const float v[4] = {acc[fm][fn][4 * g], acc[fm][fn][4 * g + 1], acc[fm][fn][4 * g + 2],
+                            acc[fm][fn][4 * g + 3]};
+        epilogue4<DT, EPI>(p, C, m, n, v, nullptr);
       }
     }
   }
