@@ -199,12 +199,13 @@ qa::Plan plan_linear(const qa_linear_desc& d, int num_cus, size_t max_ws_floats 
   // the shape, must not decide whether a valid batched call can run.
   if (d.batch > 1) forced_splits = 1;
 
-  int cands[qa::TILE_COUNT] = {qa::TILE_128x128, qa::TILE_256x128, qa::TILE_128x256,
-                               qa::TILE_64x128,  qa::TILE_64x64,   qa::TILE_128x192,
-                               qa::TILE_256x256, qa::TILE_64x64_P2};
-  int ncand = qa::TILE_COUNT;
+  // every tile shape of the plain loader (TILE_256x160 is the conv loader's)
+  int cands[] = {qa::TILE_128x128, qa::TILE_256x128, qa::TILE_128x256, qa::TILE_64x128,
+                 qa::TILE_64x64,   qa::TILE_128x192, qa::TILE_256x256, qa::TILE_64x64_P2};
+  int ncand = (int)(sizeof cands / sizeof cands[0]);
   if (pl.transb) ncand = 1;  // the conv operand path has one tile shape
-  if (forced_tile >= 0 && forced_tile < qa::TILE_COUNT && !pl.transb) {
+  if (forced_tile >= 0 && forced_tile < qa::TILE_COUNT && forced_tile != qa::TILE_256x160 &&
+      !pl.transb) {
     cands[0] = forced_tile;
     ncand = 1;
   }
@@ -299,6 +300,7 @@ double conv_stage_us(int tile) {
     case qa::TILE_128x256: return 1.09;
     case qa::TILE_256x128: return 1.21;
     case qa::TILE_256x256: return 2.27;
+    case qa::TILE_256x160: return 1.30;  // first estimate: 52 KB stages
     default: return 0.74;  // 128 x 128
   }
 }
@@ -311,7 +313,8 @@ qa::Plan plan_conv(int64_t M, int64_t N, int64_t K, bool gelu, int num_cus) {
   double best = 1e300;
   int forced_tile = -1;
   if (const char* e = getenv("QA_TILE")) forced_tile = atoi(e);
-  for (const int tile : {qa::TILE_128x256, qa::TILE_256x128, qa::TILE_128x128, qa::TILE_256x256}) {
+  for (const int tile : {qa::TILE_128x256, qa::TILE_256x128, qa::TILE_128x128, qa::TILE_256x256,
+                         qa::TILE_256x160}) {
     if (forced_tile >= 0 && forced_tile != tile) continue;
     const qa::TileShape ts = qa::tile_shape(tile);
     const int64_t tm = (M + ts.bm - 1) / ts.bm, tn = (N + ts.bn - 1) / ts.bn;

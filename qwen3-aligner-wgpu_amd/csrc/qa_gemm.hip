@@ -338,9 +338,9 @@ __device__ __forceinline__ void finish_tile(const GemmParams& p, f32x16 (&acc)[F
 // waves issue only a few MFMAs per 64 k, then meet at a barrier PL times less
 // often for the same bytes in flight.
 template <int DT, int BM, int BN, int S, int EPI, int KG, int PW, int CV = 0, int WGN = 2,
-          int PL = 1>
-__global__ void __launch_bounds__(64 * (2 * WGN * KG + PW)) gemm_dma_kernel(const GemmParams p) {
-  constexpr int WGM = 2;                     // waves along m within a group (WGN along n)
+          int PL = 1, int WGM = 2>
+__global__ void __launch_bounds__(64 * (WGM * WGN * KG + PW)) gemm_dma_kernel(const GemmParams p) {
+  // WGM waves along m within a group (WGN along n)
   constexpr int GW = WGM * WGN;              // MMA waves per k group
   constexpr int NMW = GW * KG;               // MMA waves
   constexpr int NTH = 64 * (NMW + PW);       // threads
@@ -362,7 +362,7 @@ __global__ void __launch_bounds__(64 * (2 * WGN * KG + PW)) gemm_dma_kernel(cons
   static_assert(EPI != EPI_SILU || BN % 64 == 0, "SiLU tiles hold whole gate / up subtiles");
   static_assert(S >= 2 && (S - 1) * LPS < 64, "pipeline depth");
   static_assert(KG == 1 || (KG - 1) * 4 * BM * BN <= SMEM, "reduction buffer");
-  static_assert(EP == 1 || (EP == WGM && KG == 1), "row passes follow the waves' m halves");
+  static_assert(EP == 1 || (WGM % EP == 0 && KG == 1), "row passes take whole wave rows");
   static_assert(SMEM <= 160 * 1024, "LDS");
   __shared__ __attribute__((aligned(1024))) unsigned char smem[SMEM];
 
@@ -551,7 +551,14 @@ __global__ void __launch_bounds__(64 * (2 * WGN * KG + PW)) gemm_dma_kernel(cons
       if (it + S < nk) issue(it + S, it % S);
     }
   } else if (nk > 0) {
-    if (dma_wave) {
+    // The MMA waves; they also issue the DMA only without producer waves.
+    // Known at compile time for one k group: the conv loader's per-chunk
+    // state then stays out of the MMA waves' registers (256 x 160: 256 VGPRs
+    // and a 100-byte spill before, 231 after).  The two-group 64-row tiles
+    // keep the run-time test: their o / down launches measured 9% slower
+    // with the compile-time one (same box, 11.8 -> 12.9 us).
+    const bool dma_here = KG == 1 ? PW == 0 : dma_wave;
+    if (dma_here) {
 #pragma unroll
       for (int s = 0; s < S; ++s)
         if (s < nk) issue(s, s);
@@ -572,7 +579,7 @@ __global__ void __launch_bounds__(64 * (2 * WGN * KG + PW)) gemm_dma_kernel(cons
       }
       wait_lds();  // unconditional: both paths reach the last MFMAs with ready slots
       if (it + 1 < nk) {
-        if (dma_wave) {
+        if (dma_here) {
           if (it + S - 1 < nk) {
             if (PW == 0 && pf_on && it < S - 1)
               wait_vmcnt<(S - 2) * LPS + PFI>();
@@ -588,7 +595,7 @@ __global__ void __launch_bounds__(64 * (2 * WGN * KG + PW)) gemm_dma_kernel(cons
       mma((SPG - 1) & 1);
       // Refill the freed buffer behind this wave's LDS reads and MFMAs (issued
       // ahead of them, the DMA writes measurably delay the fragment reads).
-      if (dma_wave && it + 1 < nk && it + S < nk) {
+      if (dma_here && it + 1 < nk && it + S < nk) {
         __builtin_amdgcn_sched_barrier(0);
         issue(it + S, buf);
       }
@@ -615,7 +622,7 @@ __global__ void __launch_bounds__(64 * (2 * WGN * KG + PW)) gemm_dma_kernel(cons
     if (e > 0) __syncthreads();  // the previous pass's rows have been read
 #pragma unroll
     for (int g = 0; g < KG; ++g) {
-      if (kg == g && (EP == 1 || wm == e)) {
+      if (kg == g && (EP == 1 || wm / (WGM / EP) == e)) {
         auto at = [&](int fm, int fn, int q) {
           const int row = wm * WTM + fm * 32 + fr - e * PR;
           const int col = (wn * FN + fn) * 32 + 8 * q + 4 * fh;
@@ -838,12 +845,12 @@ hipError_t launch_kernel(K k, dim3 grid, dim3 block, hipStream_t s, const Stamps
 }
 
 template <int DT, int BM, int BN, int S, int EPI, int KG, int PW, int CV = 0, int WGN = 2,
-          int PL = 1>
+          int PL = 1, int WGM = 2>
 hipError_t launch_dma(const Plan& plan, const GemmParams& p, int batch, hipStream_t s,
                       const Stamps& ts) {
   const unsigned units = (unsigned)(plan.tiles_m * plan.tiles_n * plan.splits);
-  return launch_kernel(gemm_dma_kernel<DT, BM, BN, S, EPI, KG, PW, CV, WGN, PL>,
-                       dim3(units, (unsigned)batch), dim3(64 * (2 * WGN * KG + PW)), s, ts, p);
+  return launch_kernel(gemm_dma_kernel<DT, BM, BN, S, EPI, KG, PW, CV, WGN, PL, WGM>,
+                       dim3(units, (unsigned)batch), dim3(64 * (WGM * WGN * KG + PW)), s, ts, p);
 }
 
 template <int DT, int EPI>
@@ -874,6 +881,8 @@ hipError_t launch_epi(const Plan& plan, const GemmParams& p, int batch, hipStrea
       e = launch_dma<DT, 128, 256, 3, EPI, 1, 4, 1>(plan, p, batch, s, ts);
     else if (plan.tile == TILE_256x256)
       e = launch_dma<DT, 256, 256, 2, EPI, 1, 0, 1, 4>(plan, p, batch, s, ts);
+    else if (plan.tile == TILE_256x160)  // 4 x 1 waves of 64 x 160: N = 480 in three tiles
+      e = launch_dma<DT, 256, 160, 3, EPI, 1, 4, 1, 1, 1, 4>(plan, p, batch, s, ts);
     else
       e = launch_dma<DT, 128, 128, 3, EPI, 1, 8, 1>(plan, p, batch, s, ts);
   } else if (plan.transb) {

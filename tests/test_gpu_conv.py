@@ -82,8 +82,8 @@ def test_conv(ctx, pkg, orc, dtype, b, h, w, c_in, c_out, tmajor):
     assert_parity(got, want, orc, dtype, ulp_tol=1)
 
 
-@pytest.mark.parametrize("tile", ["0", "1", "2", "6"],
-                         ids=["128x128", "256x128", "128x256", "256x256"])
+@pytest.mark.parametrize("tile", ["0", "1", "2", "6", "8"],
+                         ids=["128x128", "256x128", "128x256", "256x256", "256x160"])
 def test_conv_tiles_and_no_activation(ctx, pkg, orc, monkeypatch, tile):
     """Every implicit-GEMM tile shape, without bias and GELU (the plain sum)."""
     monkeypatch.setenv("QA_TILE", tile)
