@@ -911,6 +911,10 @@ hipError_t launch_epi(const Plan& plan, const GemmParams& p, int batch, hipStrea
       // 4352-token prefill -3%, the 300 s forward -2% (same box).
       case TILE_128x192: e = launch_dma<DT, 128, 192, 3, EPI, 1, 4>(plan, p, batch, s, ts); break;
       case TILE_256x256: e = launch_dma<DT, 256, 256, 2, EPI, 1, 0, 0, 4>(plan, p, batch, s, ts); break;
+      // 256 x 192: one round where 128 x 192 needs two (the tower's qkv at M = 3900)
+      case TILE_256x192:
+        e = launch_dma<DT, 256, 192, 2, EPI, 1, 0, 0, 2, 1, 4>(plan, p, batch, s, ts);
+        break;
       default: e = launch_dma<DT, 128, 128, 3, EPI, 1, 8>(plan, p, batch, s, ts); break;
     }
   }

@@ -26,6 +26,7 @@ enum TileCfg : int {
   TILE_256x256 = 6,  // one k group of 2x4 waves of 128(m) x 64(n)
   TILE_64x64_P2 = 7, // 64x64 with two 64-deep planes per ring stage (one barrier per 128 k)
   TILE_256x160 = 8,  // implicit-GEMM conv only: 4 x 1 waves of 64(m) x 160(n)
+  TILE_256x192 = 9,  // 4 x 2 waves of 64(m) x 96(n), two stages, MMA waves issue the DMA
   TILE_COUNT
 };
 
@@ -42,6 +43,7 @@ inline TileShape tile_shape(int cfg) {
     case TILE_128x192: return {128, 192};
     case TILE_256x256: return {256, 256};
     case TILE_256x160: return {256, 160};
+    case TILE_256x192: return {256, 192};
     default: return {128, 128};
   }
 }

@@ -182,7 +182,7 @@ def test_batched_long_k_is_never_split(ctx, pkg, orc, dtype):
 
 
 @pytest.mark.parametrize("dtype", [0, 1], ids=["f16", "bf16"])
-@pytest.mark.parametrize("tile", list(range(8)))
+@pytest.mark.parametrize("tile", [0, 1, 2, 3, 4, 5, 6, 7, 9])
 @pytest.mark.parametrize("splits", [1, 2, 3, 5])
 def test_forced_tiles_and_splits(ctx, pkg, orc, tile, splits, dtype):
     """Every tile shape, with and without split-K (incl. uneven k ranges), in
@@ -215,7 +215,8 @@ def test_forced_tiles_and_splits(ctx, pkg, orc, tile, splits, dtype):
 
 @pytest.mark.parametrize("dtype", [0, 1], ids=["f16", "bf16"])
 @pytest.mark.parametrize("group_m", [1, 3, 5, 8, 1000])
-@pytest.mark.parametrize("tile,splits", [(4, 1), (0, 1), (3, 2), (5, 1), (6, 1), (7, 1), (7, 3)])
+@pytest.mark.parametrize("tile,splits", [(4, 1), (0, 1), (3, 2), (5, 1), (6, 1), (7, 1), (7, 3),
+                                         (9, 1), (9, 2)])
 def test_tile_enumeration_bands(ctx, pkg, orc, group_m, tile, splits, dtype):
     """Every band height of the tile enumeration (including ones that do not
     divide the tile grid, and more than its height) maps blocks onto tiles
