@@ -459,7 +459,10 @@ int qa_timestamp_head(qa_ctx* ctx, const qa_head_desc* desc);
 
 /* Message of the last failure on this thread ("" if none). */
 const char* qa_last_error(void);
-/* Library version string, e.g. "qa 0.1.0 (abi 1, gfx950)". */
+/* Library version string, e.g. "qa 0.2.0 (abi 2, gfx950)".  The abi number
+ * changes whenever an exported signature changes (abi 2: qa_rope_tables takes
+ * the run's 16-bit format before its output pointers); a caller built against
+ * another abi must not bind this library. */
 const char* qa_version(void);
 
 #ifdef __cplusplus

@@ -456,6 +456,11 @@ int qah_decoder_prefill_linears(qah_decoder* d, int rows) {
   return d ? d->d->prefill_linears(rows) : QA_EINVAL;
 }
 
+int qah_decoder_layer(qah_decoder* d, int li, int rows) {
+  if (!d || li < 0 || li >= d->d->layers || rows < 0 || rows > d->d->max_rows) return QA_EINVAL;
+  return d->d->layer(li, rows);
+}
+
 int qah_decoder_read(qah_decoder* d, int which, int rows, uint16_t* host) {
   return d ? d->d->read(which, rows, host) : QA_EINVAL;
 }

@@ -66,6 +66,9 @@ int qah_decoder_set_inputs(qah_decoder* d, int rows, const uint16_t* normed,
                            const uint16_t* attn, const uint16_t* norm2, const uint16_t* h);
 /* Enqueue every layer's four projections (no wait). */
 int qah_decoder_prefill_linears(qah_decoder* d, int rows);
+/* Enqueue layer `li`'s four projections alone, with the same prefetch hints
+ * as in the whole pass (its down launch pulls layer li + 1's qkv weights). */
+int qah_decoder_layer(qah_decoder* d, int li, int rows);
 /* Copy back: which = 0 h [rows, hidden], 1 qkv [rows, q+2kv] of the last
  * layer run, 2 act [rows, inter] of the last layer run. */
 int qah_decoder_read(qah_decoder* d, int which, int rows, uint16_t* host);

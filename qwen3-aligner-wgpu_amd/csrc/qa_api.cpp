@@ -385,8 +385,28 @@ int set_device(qa_ctx* ctx) {
   return e == hipSuccess ? ok() : hip_fail(e, "hipSetDevice");
 }
 
+// What the next projection launch takes over from the context: the
+// qa_prefetch_hint range and the qa_time_next_launch events.  Every
+// projection entry point takes them first thing, before any check or early
+// return, so a hint or an event pair never outlives the call it was set for
+// (a hint left behind would make a later launch read a buffer that may have
+// been freed in between).
+struct NextLaunch {
+  const void* pf = nullptr;
+  size_t pf_bytes = 0;
+  hipEvent_t t0 = nullptr, t1 = nullptr;
+};
+NextLaunch take_next_launch(qa_ctx* ctx) {
+  NextLaunch n{ctx->pf, ctx->pf_bytes, ctx->t0, ctx->t1};
+  ctx->pf = nullptr;
+  ctx->pf_bytes = 0;
+  ctx->t0 = ctx->t1 = nullptr;
+  return n;
+}
+
 // Launch a validated, planned projection with split-K partials in `ws`.
-int launch_linear(qa_ctx* ctx, const qa_linear_desc* d, const qa::Plan& plan, float* ws) {
+int launch_linear(qa_ctx* ctx, const qa_linear_desc* d, const qa::Plan& plan, float* ws,
+                  const NextLaunch& nl) {
   qa::GemmParams p{};
   p.a = (const uint16_t*)d->a;
   p.w = (const uint16_t*)d->w;
@@ -412,14 +432,11 @@ int launch_linear(qa_ctx* ctx, const qa_linear_desc* d, const qa::Plan& plan, fl
   p.accumulate = (d->flags & QA_ACCUMULATE) ? 1 : 0;
   p.bias_rows = (d->flags & QA_BIAS_ROWS) ? 1 : 0;
   p.group_m = plan.group_m;
-  if (ctx->pf && !plan.transb) {
-    p.pf = (const uint16_t*)ctx->pf;
-    p.pf_bytes = (int)std::min<size_t>(ctx->pf_bytes, (size_t)INT32_MAX & ~(size_t)127);
+  if (nl.pf && !plan.transb) {
+    p.pf = (const uint16_t*)nl.pf;
+    p.pf_bytes = (int)std::min<size_t>(nl.pf_bytes, (size_t)INT32_MAX & ~(size_t)127);
   }
-  ctx->pf = nullptr;
-  ctx->pf_bytes = 0;
-  const hipEvent_t t0 = ctx->t0, t1 = ctx->t1;
-  ctx->t0 = ctx->t1 = nullptr;
+  const hipEvent_t t0 = nl.t0, t1 = nl.t1;
   if (t0 || t1) {
     // a captured dispatch does not stamp them on replay (the graph keeps an
     // event node that reads back as garbage)
@@ -442,7 +459,7 @@ extern "C" {
 
 const char* qa_last_error(void) { return g_err.c_str(); }
 
-const char* qa_version(void) { return "qa 0.1.0 (abi 1, gfx950)"; }
+const char* qa_version(void) { return "qa 0.2.0 (abi 2, gfx950)"; }
 
 int qa_ctx_create(int device, qa_ctx** out) {
   if (!out) return fail(QA_EINVAL, "qa_ctx_create: null output pointer");
@@ -551,6 +568,7 @@ int qa_linear_validate(const qa_linear_desc* desc) { return validate(desc); }
 
 int qa_linear(qa_ctx* ctx, const qa_linear_desc* d) {
   if (!ctx) return fail(QA_EINVAL, "qa_linear: null context");
+  const NextLaunch nl = take_next_launch(ctx);
   if (int rc = validate(d)) return rc;
   if (d->m == 0) return ok();
   if (int rc = set_device(ctx)) return rc;
@@ -558,11 +576,12 @@ int qa_linear(qa_ctx* ctx, const qa_linear_desc* d) {
   if (plan.splits > 1) {
     if (int rc = ensure_workspace(ctx, plan.ws_floats)) return rc;
   }
-  return launch_linear(ctx, d, plan, ctx->ws);
+  return launch_linear(ctx, d, plan, ctx->ws, nl);
 }
 
 int qa_linear_noalloc(qa_ctx* ctx, const qa_linear_desc* d) {
   if (!ctx) return fail(QA_EINVAL, "qa_linear_noalloc: null context");
+  const NextLaunch nl = take_next_launch(ctx);
   if (int rc = validate(d)) return rc;
   if (d->m == 0) return ok();
   if (int rc = set_device(ctx)) return rc;
@@ -574,7 +593,7 @@ int qa_linear_noalloc(qa_ctx* ctx, const qa_linear_desc* d) {
                 "qa_linear_noalloc: %d K splits of a %lld x %lld output need %zu f32 partials; the "
                 "scratch holds %zu",
                 plan.splits, (long long)d->m, (long long)d->n, plan.ws_floats, kScratchFloats);
-  return launch_linear(ctx, d, plan, ctx->scratch);
+  return launch_linear(ctx, d, plan, ctx->scratch, nl);
 }
 
 size_t qa_linear_noalloc_scratch_floats(void) { return kScratchFloats; }
@@ -595,7 +614,11 @@ int qa_time_next_launch(qa_ctx* ctx, void* start_event, void* stop_event) {
 }
 
 int qa_mlp_fused(qa_ctx* ctx, const qa_mlp_desc* d) {
-  if (!ctx || !d) return fail(QA_EINVAL, "qa_mlp_fused: null argument");
+  if (!ctx) return fail(QA_EINVAL, "qa_mlp_fused: null context");
+  // the caller's hint and timing events belong to this call whatever happens
+  // below; they go to the gate|up launch
+  const NextLaunch nl = take_next_launch(ctx);
+  if (!d) return fail(QA_EINVAL, "qa_mlp_fused: null descriptor");
   if (d->flags) return fail(QA_EINVAL, "qa_mlp_fused: flags must be 0");
   if (d->m < 0 || d->hidden <= 0 || d->inter <= 0)
     return fail(QA_EINVAL, "qa_mlp_fused: bad shape");
@@ -627,10 +650,13 @@ int qa_mlp_fused(qa_ctx* ctx, const qa_mlp_desc* d) {
   down.batch = 1;
   if (int rc = validate(&gu)) return rc;
   if (int rc = validate(&down)) return rc;
+  if (d->m == 0) return ok();
   // a caller's hint stays with the gate|up launch; otherwise it pulls the
   // down projection's weights toward the caches
-  if (!ctx->pf)
-    if (int rc = qa_prefetch_hint(ctx, d->w_down, (size_t)(d->hidden * d->inter) * 2)) return rc;
+  ctx->pf = nl.pf ? nl.pf : d->w_down;
+  ctx->pf_bytes = nl.pf ? nl.pf_bytes : (size_t)(d->hidden * d->inter) * 2;
+  ctx->t0 = nl.t0;
+  ctx->t1 = nl.t1;
   if (int rc = qa_linear(ctx, &gu)) return rc;
   return qa_linear(ctx, &down);
 }

@@ -30,6 +30,7 @@ def declare(L: ctypes.CDLL) -> None:
     L.qah_decoder_load_layer.argtypes = [_vp, _i] + [_vp] * 7
     L.qah_decoder_set_inputs.argtypes = [_vp, _i, _vp, _vp, _vp, _vp]
     L.qah_decoder_prefill_linears.argtypes = [_vp, _i]
+    L.qah_decoder_layer.argtypes = [_vp, _i, _i]
     L.qah_decoder_read.argtypes = [_vp, _i, _i, _vp]
     L.qah_decoder_time.argtypes = [_vp, _i, _i, _i, _i, _dp, _dp]
     L.qah_decoder_profile_sites.argtypes = [_vp, _i, _i, _dp]
@@ -289,6 +290,10 @@ class DecoderLinears:
 
     def prefill_linears(self, rows):
         check(host_lib().qah_decoder_prefill_linears(self.handle, rows))
+
+    def layer(self, li, rows):
+        """One layer's four projections (as prefill_linears runs them)."""
+        check(host_lib().qah_decoder_layer(self.handle, li, rows))
 
     def read(self, which: str, rows: int) -> np.ndarray:
         idx, cols = {"h": (0, self.hidden), "qkv": (1, self.q_dim + 2 * self.kv_dim),

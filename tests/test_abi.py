@@ -41,7 +41,7 @@ def test_host_mirror_exports(pkg):
 
 def test_version(pkg):
     v = pkg.version()
-    assert "abi 1" in v and "gfx950" in v
+    assert "abi 2" in v and "gfx950" in v
 
 
 def _desc(pkg, **kw):

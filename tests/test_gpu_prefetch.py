@@ -39,10 +39,21 @@ def _linear(ctx, pkg, dtype, da, dw, dc, m, n, k, ldc, flags, db, hint):
     ctx.linear(pkg.linear_desc(dtype, m, n, k, da, dw, dc, flags=flags, bias=db, ldc=ldc))
 
 
+# TILE_256x192 (9) has a 2-stage ring whose MMA waves issue their own DMA:
+# the prefetch loads share their vmcnt stream; k = 64 is shorter than its ring.
 @pytest.mark.parametrize("dtype", [0, 1], ids=["f16", "bf16"])
 @pytest.mark.parametrize("k", [128, 1216])
-@pytest.mark.parametrize("tile,splits", [(t, 1) for t in range(8)] + [(5, 3), (7, 2)])
+@pytest.mark.parametrize("tile,splits", [(t, 1) for t in range(8)] + [(5, 3), (7, 2), (9, 1), (9, 2)])
 def test_hint_leaves_results_unchanged(ctx, pkg, orc, hint_buf, tile, splits, k, dtype):
+    _hint_case(ctx, pkg, orc, hint_buf, tile, splits, k, dtype)
+
+
+@pytest.mark.parametrize("dtype", [0, 1], ids=["f16", "bf16"])
+def test_hint_with_k_shorter_than_the_ring(ctx, pkg, orc, hint_buf, dtype):
+    _hint_case(ctx, pkg, orc, hint_buf, 9, 1, 64, dtype)
+
+
+def _hint_case(ctx, pkg, orc, hint_buf, tile, splits, k, dtype):
     rng = np.random.default_rng(7000 + 10 * tile + splits + k + dtype)
     m, n = 300, 512
     a = _h16(orc, rng.standard_normal((m, k)), dtype)
@@ -85,6 +96,69 @@ def test_hint_arguments(ctx, pkg, hint_buf):
     # a hint a projection never takes over (no launch follows) is harmless
     ctx.prefetch_hint(hint_buf, 100)
     ctx.sync()
+    assert lib.qa_prefetch_hint(ctx.handle, None, 0) == pkg.QA_OK  # leave none behind
+
+
+def _events(n):
+    import ctypes
+    from hipgraph import hip
+    L = hip()
+    L.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+    L.hipEventDestroy.argtypes = [ctypes.c_void_p]
+    ev = [ctypes.c_void_p() for _ in range(n)]
+    for e in ev:
+        assert L.hipEventCreate(ctypes.byref(e)) == 0
+    return ev
+
+
+def test_calls_that_launch_nothing_drop_the_hint_and_events(pkg, orc):
+    """A hint and timing events set before a call that launches nothing (m = 0,
+    a refused descriptor, a fused MLP of zero rows) end with that call: the
+    hinted buffer is freed afterwards, and the next projection is captured
+    into a graph (which refuses leftover timing events) and replays to the
+    same bits as an eager launch."""
+    from hipgraph import Capture, hip
+    rng = np.random.default_rng(78)
+    m, n, k = 256, 512, 1024
+    a = _h16(orc, rng.standard_normal((m, k)), 0)
+    w = _h16(orc, 0.02 * rng.standard_normal((n, k)), 0)
+    with pkg.Context(0) as fresh:
+        lib = pkg.lib()
+        da, dw = fresh.to_device(a), fresh.to_device(w)
+        dc, want_buf = fresh.alloc(m * n * 2), fresh.alloc(m * n * 2)
+        fresh.linear(pkg.linear_desc(0, m, n, k, da, dw, want_buf))
+        want = fresh.download(want_buf, (m, n))
+        ev = _events(2)
+        try:
+            bad = pkg.linear_desc(0, m, n, 12, da, dw, dc)  # k not a multiple of 8
+            zero = pkg.linear_desc(0, 0, n, k, da, dw, dc)
+            mlp0 = pkg.MlpDesc(dtype=0, flags=0, m=0, hidden=k, inter=n, x=da.ptr, w_gu=dw.ptr,
+                               w_down=dw.ptr, act=dc.ptr, h=want_buf.ptr)
+            calls = [lambda: fresh.linear(zero), lambda: fresh.linear_noalloc(zero),
+                     lambda: fresh.mlp_fused(mlp0)]
+            for call in calls + ["bad"]:
+                doomed = fresh.alloc(8 << 20)
+                fresh.prefetch_hint(doomed)
+                pkg.check(lib.qa_time_next_launch(fresh.handle, ev[0], ev[1]))
+                if call == "bad":
+                    with pytest.raises(pkg.QAError):
+                        fresh.linear(bad)
+                else:
+                    call()
+                doomed.free()
+                fresh.sync()
+                with Capture(fresh.stream) as cap:
+                    fresh.linear(pkg.linear_desc(0, m, n, k, da, dw, dc))
+                try:
+                    for _ in range(3):
+                        fresh.upload(dc, np.zeros((m, n), np.uint16))
+                        cap.replay()
+                        assert np.array_equal(fresh.download(dc, (m, n)), want)
+                finally:
+                    cap.close()
+        finally:
+            for e in ev:
+                hip().hipEventDestroy(e)
 
 
 def test_fused_mlp_with_and_without_a_caller_hint(ctx, pkg, orc, hint_buf):

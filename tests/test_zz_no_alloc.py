@@ -1,7 +1,9 @@
 """qa_linear_noalloc (the allocation-free linear) against qa_linear through
 the C ABI: two calls in a row, the second with a smaller input, each with
 split-K forced so the partials go through the fixed device scratch, must give
-outputs identical to qa_linear's (same kernels, same split order); a forced
+outputs identical to qa_linear's (same kernels, same split order).  The
+allocation-free call runs first, on a fresh context that has never sized a
+workspace, under stream capture, so a call that allocated would fail.  A forced
 split whose partials exceed the scratch is refused with QA_EINVAL; without a
 forced split the planner keeps within the scratch on its own.  Runs alone in a
 fresh process and after the other tests (the scratch keeps the previous
@@ -20,23 +22,43 @@ def _h16(orc, x, dtype):
     return orc.h16_from_f32(np.asarray(x, np.float32), dtype)
 
 
+def _run(c, fn, pkg, dtype, a, w, c0, flags, bias, splits, capture=False):
+    da, dw, dc = c.to_device(a), c.to_device(w), c.to_device(c0)
+    db = c.to_device(bias) if bias is not None else None
+    m, k = a.shape
+    n = w.shape[0]
+    desc = pkg.linear_desc(dtype, m, n, k, da, dw, dc, flags=flags, bias=db, ldc=c0.shape[1])
+    os.environ["QA_SPLITS"] = str(splits)
+    try:
+        if capture:
+            # recorded into a graph: a call that allocated (or grew the
+            # context's workspace, which refuses to under capture) would fail
+            from hipgraph import Capture
+            with Capture(c.stream) as cap:
+                fn(desc)
+            try:
+                cap.replay()
+            finally:
+                cap.close()
+        else:
+            fn(desc)
+    finally:
+        del os.environ["QA_SPLITS"]
+    out = c.download(dc, c0.shape)
+    for b in (da, dw, dc, db):
+        if b is not None:
+            b.free()
+    return out
+
+
 def _both(ctx, pkg, dtype, a, w, c0, flags, bias, splits):
-    outs = []
-    for fn in (ctx.linear, ctx.linear_noalloc):
-        da, dw, dc = ctx.to_device(a), ctx.to_device(w), ctx.to_device(c0)
-        db = ctx.to_device(bias) if bias is not None else None
-        m, k = a.shape
-        n = w.shape[0]
-        os.environ["QA_SPLITS"] = str(splits)
-        try:
-            fn(pkg.linear_desc(dtype, m, n, k, da, dw, dc, flags=flags, bias=db, ldc=c0.shape[1]))
-        finally:
-            del os.environ["QA_SPLITS"]
-        outs.append(ctx.download(dc, c0.shape))
-        for b in (da, dw, dc, db):
-            if b is not None:
-                b.free()
-    return outs
+    """qa_linear on the session context, and qa_linear_noalloc FIRST on a fresh
+    context that has never sized a workspace, under stream capture."""
+    with pkg.Context(0) as fresh:
+        got = _run(fresh, fresh.linear_noalloc, pkg, dtype, a, w, c0, flags, bias, splits,
+                   capture=True)
+    want = _run(ctx, ctx.linear, pkg, dtype, a, w, c0, flags, bias, splits)
+    return want, got
 
 
 @pytest.mark.parametrize("dtype", [0, 1], ids=["f16", "bf16"])
