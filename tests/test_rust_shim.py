@@ -5,7 +5,13 @@ here) against include/qa.h, mechanically:
     from the field types) equal to offsetof / sizeof from a C program compiled
     from qa.h;
   * every `pub fn qa_*` in the `extern "C"` block: declared in qa.h with the
-    same parameter and return types, and every qa.h function is bound.
+    same parameter and return types, and every qa.h function is bound;
+  * the status-code constants equal qa.h's enum, and `open_towers` maps the
+    crate's device policy (`gpu::Backend`, src/gpu.rs:121-153) as
+    `load_backend_with_dtype` does (src/align_inference.rs:331-345): `Auto`
+    falls back to the CPU towers on QA_EDEVICE / QA_EUNSUPPORTED only, `Gpu`
+    returns every error, `Cpu` opens nothing, and every DeviceSelector
+    variant (src/gpu.rs:30-51) is handled.
 """
 from __future__ import annotations
 
@@ -125,3 +131,52 @@ def test_rust_functions_match_the_c_prototypes():
     assert set(rust) == set(c), (sorted(set(c) - set(rust)), sorted(set(rust) - set(c)))
     for name, sig in rust.items():
         assert sig == c[name], (name, sig, c[name])
+
+
+def _rust_block(text, start):
+    """The brace-balanced block that follows `start` in text."""
+    i = text.index(start)
+    j = text.index("{", i)
+    depth = 0
+    for k in range(j, len(text)):
+        depth += {"{": 1, "}": -1}.get(text[k], 0)
+        if depth == 0:
+            return text[j + 1:k]
+    raise AssertionError(f"unbalanced block after {start}")
+
+
+def _arm(body, pattern):
+    """Text of the match arm starting at `pattern`, up to the next top-level arm."""
+    m = re.search(pattern, body)
+    assert m, pattern
+    rest = body[m.end():]
+    nxt = re.search(r"\n        Backend::\w+", rest)
+    return rest[:nxt.start()] if nxt else rest
+
+
+def test_status_constants_match_the_header():
+    doc = open(DOC).read()
+    rust = {n: int(v) for n, v in re.findall(r"pub const (QA_E\w+|QA_OK): c_int = (-?\d+);", doc)}
+    hdr = re.sub(r"/\*.*?\*/", "", open(HDR).read(), flags=re.S)
+    c = {n: int(v) for n, v in re.findall(r"\b(QA_E[A-Z]+|QA_OK)\s*=\s*(-?\d+)\s*[,}]", hdr)}
+    assert rust == c and len(c) == 5, (rust, c)
+
+
+def test_backend_policy_binding():
+    doc = open(DOC).read()
+    body = _rust_block(doc, "pub fn open_towers(")
+    cpu = _arm(body, r"Backend::Cpu\s*=>")
+    assert "Towers::Cpu" in cpu and "QaGpu" not in cpu
+    auto = _arm(body, r"Backend::Auto\s*=>")
+    assert "QaGpu::open(" in auto
+    fallback = re.search(r"Err\(e\) if (.*?)=>\s*\{(.*?)\n\s*\}", auto, re.S)
+    assert fallback, auto
+    assert set(re.findall(r"QA_E\w+", fallback.group(1))) == {"QA_EDEVICE", "QA_EUNSUPPORTED"}
+    assert "Ok(Towers::Cpu)" in fallback.group(2)
+    assert re.search(r"Err\(e\)\s*=>\s*Err\(", auto), "other errors must be returned"
+    gpu = _arm(body, r"Backend::Gpu\(sel\)\s*=>")
+    assert "Towers::Cpu" not in gpu, "Backend::Gpu never falls back"
+    assert "?" in gpu and "QaGpu::open(" in gpu
+    # every DeviceSelector variant of src/gpu.rs:30-51 is handled
+    for variant in ("Auto", "Runtime", "Cpu", "Index", "Name"):
+        assert re.search(r"DeviceSelector::" + variant + r"\b", gpu), variant
