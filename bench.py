@@ -379,6 +379,8 @@ def site_descs(pkg, host, ctx, site, warm):
         m, n, k, fl, xk = 512, 2 * it, h, 2, None
     elif site == "config2_down":
         m, n, k, fl, xk = 512, h, it, 1, None
+    elif site == "config2_mlp":
+        return config2_pair_descs(pkg, host, ctx, warm)
     elif site in sites:
         (n, k, fl), m = sites[site], 1024
         xk = k
@@ -396,6 +398,22 @@ def site_descs(pkg, host, ctx, site, warm):
         flags = {0: 0, 1: pkg.ACCUMULATE, 2: pkg.EPI_SILU_MUL}[fl]
         descs.append(pkg.linear_desc(pkg.F16, m, n, k, a, w, c, flags=flags, ldc=nout))
     return descs, 2 * m * n * k
+
+
+def config2_pair_descs(pkg, host, ctx, warm):
+    """Config 2's MLP block as launch pairs (gate|up + SiLU.up, then down +
+    residual, M = 512): warm one weight set, cold 16 distinct sets (320 MB).
+    Returns (descriptors in launch order, FLOPs per pair)."""
+    m, hid, it = 512, DEC["hidden"], DEC["inter"]
+    x = ctx.to_device(host.synth_normal(0, 21, (m, hid)))
+    act = ctx.alloc(m * it * 2)
+    descs = []
+    for i in range(1 if warm else 16):
+        gu = ctx.to_device(host.synth_normal(0, 22 if i == 0 else 2200 + 2 * i, (2 * it, hid), 0, 0.02))
+        dn = ctx.to_device(host.synth_normal(0, 23 if i == 0 else 2201 + 2 * i, (hid, it), 0, 0.02))
+        descs += [pkg.linear_desc(pkg.F16, m, 2 * it, hid, x, gu, act, flags=pkg.EPI_SILU_MUL),
+                  pkg.linear_desc(pkg.F16, m, hid, it, act, dn, x, flags=pkg.ACCUMULATE)]
+    return descs, 2 * m * 2 * it * hid + 2 * m * hid * it
 
 
 def config1_protocol(pkg, host, ctx):
@@ -621,7 +639,8 @@ def main():
     ap.add_argument("--site", default=None,
                     help="only launch one GEMM site --launches times (for rocprofv3 counter runs): "
                          "qkv, o, gu, down (fused), q, k, v, gate, up (unfused) over the 28 layers' "
-                         "weights, or config1")
+                         "weights, config1, config2_gu, config2_down, or config2_mlp (gate|up, down "
+                         "pairs; --launches counts launches, the figures are per pair)")
     ap.add_argument("--launches", type=int, default=56)
     ap.add_argument("--warm", action="store_true",
                     help="with --site: repeat layer 0's (or config 1's first) W instead of cycling")
@@ -647,6 +666,8 @@ def main():
         with pkg.Context(0) as ctx:
             descs, flops = site_descs(pkg, host, ctx, args.site, args.warm)
             ms = host.time_linears_each(ctx, descs, 0, args.launches)
+            if args.site == "config2_mlp":  # launch pairs: per-pair figures
+                ms = ms[0::2] + ms[1::2]
             print(json.dumps({"site": args.site, "warm": args.warm, "weight_sets": len(descs),
                               "flops_per_launch": flops, "per_launch": dist(ms)}), flush=True)
         return
