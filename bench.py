@@ -28,6 +28,7 @@ other BASELINE configs (1, 2, 4) as kernel-level figures.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -400,6 +401,57 @@ def site_descs(pkg, host, ctx, site, warm):
     return descs, 2 * m * n * k
 
 
+def phase_stamps(pkg, host, ctx, warmup, steps):
+    """Config 3 in a graph replay on the measurement build: the per-block
+    s_memrealtime records (100 MHz) of the last 8 GEMM launches (the last two
+    layers: qkv, o, gate|up, down), reduced per launch to medians over its
+    blocks (us): gap from the previous launch's last block end, start skew
+    (first to last block start), fill (start to ring stage 0 in), main loop,
+    park (accumulators to LDS), stores (first store to block end), span."""
+    L = pkg.lib()
+    L.qa_phase_stamps_read.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+    slots, blocks = ctypes.c_int(), ctypes.c_int()
+    L.qa_phase_stamps_read(None, ctypes.byref(slots), ctypes.byref(blocks))
+    m = 1024
+    dec = host.DecoderLinears(ctx, pkg.F16, DEC["layers"], m, DEC["hidden"], DEC["q_dim"],
+                              DEC["kv_dim"], DEC["inter"])
+    for li in range(DEC["layers"]):
+        w = decoder_weights(host, li)
+        dec.load_layer(li, w["q"], w["k"], w["v"], w["o"], w["gate"], w["up"], w["down"])
+    dec.set_inputs(m, rmsnormed(host, 0, 1, (m, DEC["hidden"]), 0),
+                   rmsnormed(host, 0, 2, (m, DEC["q_dim"]), 0),
+                   rmsnormed(host, 0, 3, (m, DEC["hidden"]), 0),
+                   host.synth_normal(0, 4, (m, DEC["hidden"])))
+    dec.time(m, max(1, warmup), 1, use_graph=True)  # capture; the records' slots are fixed then
+    pkg.check(L.qa_phase_stamps_clear())
+    ms, _ = dec.time(m, 0, max(1, steps), use_graph=True)
+    rec = np.zeros((slots.value, blocks.value, 8), np.uint64)
+    pkg.check(L.qa_phase_stamps_read(rec.ctypes.data, None, None))
+    dec.close()
+    names = {(4096, 1024): "qkv", (1024, 2048): "o", (6144, 1024): "gu", (1024, 3072): "down"}
+    launches = []
+    for sl in range(slots.value):
+        r = rec[sl][rec[sl][:, 0] > 0].astype(np.int64)
+        if len(r):
+            launches.append(r)
+    launches.sort(key=lambda r: int(r[:, 0].min()))
+    out, prev_end = [], None
+    med = lambda x: round(float(np.median(x)) / 100.0, 2)  # noqa: E731  (100 MHz ticks -> us)
+    for r in launches:
+        t = [r[:, i] for i in range(5)]
+        out.append({"site": names.get((int(r[0, 6]), int(r[0, 7])), f"N{r[0, 6]}K{r[0, 7]}"),
+                    "blocks": int(len(r)),
+                    "gap": None if prev_end is None else round((int(t[0].min()) - prev_end) / 100.0, 2),
+                    "start_skew": round(int(t[0].max() - t[0].min()) / 100.0, 2),
+                    "fill": med(t[1] - t[0]), "loop": med(t[2] - t[1]), "park": med(t[3] - t[2]),
+                    "stores": med(t[4] - t[3]),
+                    "span": round(int(t[4].max() - t[0].min()) / 100.0, 2)})
+        prev_end = int(t[4].max())
+    return {"phase_stamps_config3": out, "step_ms": round(ms, 4),
+            "note": "measurement build (-DQA_PHASE_STAMPS); medians over blocks, us; the last "
+                    "two layers of the last graph replay"}
+
+
 def config2_pair_descs(pkg, host, ctx, warm):
     """Config 2's MLP block as launch pairs (gate|up + SiLU.up, then down +
     residual, M = 512): warm one weight set, cold 16 distinct sets (320 MB).
@@ -642,6 +694,10 @@ def main():
                          "weights, config1, config2_gu, config2_down, or config2_mlp (gate|up, down "
                          "pairs; --launches counts launches, the figures are per pair)")
     ap.add_argument("--launches", type=int, default=56)
+    ap.add_argument("--phase-stamps", action="store_true",
+                    help="config 3 on the measurement build (make -C qwen3-aligner-wgpu_amd/csrc "
+                         "stamps): per-block phase timestamps of the last two layers' GEMMs in a "
+                         "graph replay, as a table of medians (one JSON line)")
     ap.add_argument("--warm", action="store_true",
                     help="with --site: repeat layer 0's (or config 1's first) W instead of cycling")
     args = ap.parse_args()
@@ -651,6 +707,8 @@ def main():
               "token rows with no exchange; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
+    if args.phase_stamps:
+        os.environ["QA_BUILD"] = "stamps"  # before the package loads its libraries
     import __graft_entry__ as entry
 
     pkg = entry.load_package()
@@ -670,6 +728,11 @@ def main():
                 ms = ms[0::2] + ms[1::2]
             print(json.dumps({"site": args.site, "warm": args.warm, "weight_sets": len(descs),
                               "flops_per_launch": flops, "per_launch": dist(ms)}), flush=True)
+        return
+
+    if args.phase_stamps:
+        with pkg.Context(0) as ctx:
+            print(json.dumps(phase_stamps(pkg, host, ctx, args.warmup, args.steps)), flush=True)
         return
 
     if args.e2e_only:

@@ -20,8 +20,11 @@ import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(_HERE, "csrc")
-LIB_PATH = os.path.join(CSRC, "libqa.so")
-HOST_LIB_PATH = os.path.join(CSRC, "libqa_host.so")
+# QA_BUILD=stamps loads the measurement build of `make -C csrc stamps` (the
+# same libraries with per-block phase stamps in the GEMM kernels).
+_BUILD_DIR = os.path.join(CSRC, os.environ["QA_BUILD"]) if os.environ.get("QA_BUILD") else CSRC
+LIB_PATH = os.path.join(_BUILD_DIR, "libqa.so")
+HOST_LIB_PATH = os.path.join(_BUILD_DIR, "libqa_host.so")
 INCLUDE_DIR = os.path.join(os.path.dirname(_HERE), "include")
 
 # include/qa.h constants

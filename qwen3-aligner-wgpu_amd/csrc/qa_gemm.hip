@@ -48,6 +48,17 @@
 #include "qa_internal.h"
 
 namespace qa {
+
+#ifdef QA_PHASE_STAMPS
+// Measurement build only (make stamps): every block of a gemm_dma_kernel
+// launch records s_memrealtime (100 MHz) at its start, when ring stage 0 is
+// in (after the first barrier), after the main loop, after the park (the
+// first store) and at its end, plus its CU id and the launch's N and K, in
+// record slot p.stamp_slot; the host cycles the slots launch by launch.
+constexpr int kStampSlots = 8, kStampBlocks = 2048, kStampWords = 8;
+__device__ unsigned long long stamp_log[kStampSlots * kStampBlocks * kStampWords];
+#endif
+
 namespace {
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -376,6 +387,9 @@ __global__ void __launch_bounds__(64 * (WGM * WGN * KG + PW)) gemm_dma_kernel(co
   const int wm = w4 % WGM, wn = w4 / WGM;
   const int fr = lane & 31, fh = lane >> 5;  // fragment row, k-chunk parity
 
+#ifdef QA_PHASE_STAMPS
+  unsigned long long st[5] = {__builtin_amdgcn_s_memrealtime(), 0, 0, 0, 0};
+#endif
   int tm, tn, split;
   tile_of(p, (int)blockIdx.x, tm, tn, split);
   const int64_t z = blockIdx.y;
@@ -568,6 +582,9 @@ __global__ void __launch_bounds__(64 * (WGM * WGN * KG + PW)) gemm_dma_kernel(co
         wait_vmcnt<0>();
     }
     exec_barrier();
+#ifdef QA_PHASE_STAMPS
+    st[1] = __builtin_amdgcn_s_memrealtime();
+#endif
     if (pf_on) prefetch();
     read_frags(0, kk0, 0);
     for (int it = 0; it < nk; ++it) {
@@ -617,6 +634,9 @@ __global__ void __launch_bounds__(64 * (WGM * WGN * KG + PW)) gemm_dma_kernel(co
   const int nfull = EPI == EPI_SILU ? p.N / 2 : p.N;
   const int n0 = tn * OUTC;
   __syncthreads();  // all stages consumed (every DMA was waited for)
+#ifdef QA_PHASE_STAMPS
+  st[2] = __builtin_amdgcn_s_memrealtime();
+#endif
 #pragma unroll
   for (int e = 0; e < EP; ++e) {
     if (e > 0) __syncthreads();  // the previous pass's rows have been read
@@ -653,6 +673,9 @@ __global__ void __launch_bounds__(64 * (WGM * WGN * KG + PW)) gemm_dma_kernel(co
       }
       __syncthreads();
     }
+#ifdef QA_PHASE_STAMPS
+    if (e == 0) st[3] = __builtin_amdgcn_s_memrealtime();
+#endif
 #pragma unroll
     for (int it = 0; it < (PR * GPR + NTH - 1) / NTH; ++it) {
       const int idx = it * NTH + tid;
@@ -680,6 +703,18 @@ __global__ void __launch_bounds__(64 * (WGM * WGN * KG + PW)) gemm_dma_kernel(co
 #pragma unroll
     for (int i = 0; i < PFI; ++i) asm volatile("" ::"v"(pfv[i]));
   }
+#ifdef QA_PHASE_STAMPS
+  __syncthreads();  // every wave's stores issued
+  const unsigned b = blockIdx.x + blockIdx.y * gridDim.x;
+  if (tid == 0 && b < (unsigned)kStampBlocks) {
+    st[4] = __builtin_amdgcn_s_memrealtime();
+    unsigned long long* d = stamp_log + ((size_t)p.stamp_slot * kStampBlocks + b) * kStampWords;
+    for (int i = 0; i < 5; ++i) d[i] = st[i];
+    d[5] = (unsigned long long)__smid();
+    d[6] = (unsigned long long)p.N;
+    d[7] = (unsigned long long)p.K;
+  }
+#endif
 }
 
 // W as [K, N] (row stride ldb): register-staged, double-buffered; each
@@ -934,11 +969,40 @@ hipError_t launch_dt(const Plan& plan, const GemmParams& p, int batch, hipStream
 
 }  // namespace
 
-hipError_t launch_gemm(int dtype, const Plan& plan, const GemmParams& p, int batch,
+#ifdef QA_PHASE_STAMPS
+static int g_stamp_next = 0;  // the next launch's record slot
+#endif
+
+hipError_t launch_gemm(int dtype, const Plan& plan, const GemmParams& p_in, int batch,
                        hipStream_t stream, hipEvent_t t0, hipEvent_t t1) {
   const Stamps ts{t0, t1};
+#ifdef QA_PHASE_STAMPS
+  GemmParams p = p_in;
+  p.stamp_slot = g_stamp_next;
+  g_stamp_next = (g_stamp_next + 1) % kStampSlots;
+#else
+  const GemmParams& p = p_in;
+#endif
   if (dtype == QA_BF16) return launch_dt<QA_BF16>(plan, p, batch, stream, ts);
   return launch_dt<QA_F16>(plan, p, batch, stream, ts);
 }
 
 }  // namespace qa
+
+#ifdef QA_PHASE_STAMPS
+// The measurement build's stamp records: kStampSlots x kStampBlocks x 8
+// words (see stamp_log), copied to `out`; *slots, *blocks get the sizes.
+extern "C" int qa_phase_stamps_read(unsigned long long* out, int* slots, int* blocks) {
+  if (slots) *slots = qa::kStampSlots;
+  if (blocks) *blocks = qa::kStampBlocks;
+  if (!out) return QA_OK;
+  const hipError_t e = hipMemcpyFromSymbol(out, HIP_SYMBOL(qa::stamp_log), sizeof(qa::stamp_log));
+  return e == hipSuccess ? QA_OK : QA_EDEVICE;
+}
+// Zeroes every record (synchronous; call outside stream capture).
+extern "C" int qa_phase_stamps_clear(void) {
+  static unsigned long long zeros[sizeof(qa::stamp_log) / 8];
+  const hipError_t e = hipMemcpyToSymbol(HIP_SYMBOL(qa::stamp_log), zeros, sizeof(qa::stamp_log));
+  return e == hipSuccess ? QA_OK : QA_EDEVICE;
+}
+#endif

@@ -90,6 +90,9 @@ struct GemmParams {
   // cache while this one runs; pf_bytes = 0 for none (qa_prefetch_hint).
   const uint16_t* pf;
   int pf_bytes;
+#ifdef QA_PHASE_STAMPS
+  int stamp_slot;  // record slot of this launch's phase stamps (qa_gemm.hip)
+#endif
 };
 
 struct Plan {
