@@ -826,7 +826,7 @@ def main():
         log(f"[bench] aligner forward 300 s: {e2e}")
     ctx.close()
 
-    traffic, traffic_kernel, busy_pct, busy_pct_gui = measured_counters("gu")
+    traffic, traffic_kernel, busy_pct, _ = measured_counters("gu")
     cpu = None
     if args.cpu_budget > 0:
         orc = entry.load_oracle()
@@ -868,7 +868,6 @@ def main():
             "traffic": traffic,
             "traffic_kernel": traffic_kernel,
             "mfma_busy_pct": busy_pct,
-            "mfma_busy_pct_over_gui_active": busy_pct_gui,
             "counter_source": "profiles/gemm_sites_counters.md" if traffic else None,
         },
         "cpu_baseline": cpu,
