@@ -206,10 +206,17 @@ __device__ __forceinline__ void widen4(u32x2 w, float* v) {
 }
 
 // Final values of 4 consecutive output columns [n, n+4) of row m -> C.
-// For SiLU, v holds the gate sums and u the up sums.
+// For SiLU, v holds the gate sums and u the up sums.  pre_old, when given,
+// holds the group's residual words, loaded earlier; otherwise they are read
+// here.  (The loads stay inside their branches: hoisting them out of the
+// `accumulate` / `bias` tests makes the compiler wait for every outstanding
+// VMEM operation before each store, the previous groups' stores included,
+// since vmcnt counts stores too; the qkv store phase measured 2.0 against
+// 1.16 us that way.)
 template <int DT, int EPI>
 __device__ __forceinline__ void epilogue4(const GemmParams& p, uint16_t* C, int m, int n,
-                                          const float* v_in, const float* u_in) {
+                                          const float* v_in, const float* u_in,
+                                          const u32x2* pre_old = nullptr) {
   uint16_t* dst = C + (int64_t)m * p.ldc + n;
   float v[4];
   if constexpr (EPI == EPI_SILU) {
@@ -240,7 +247,7 @@ __device__ __forceinline__ void epilogue4(const GemmParams& p, uint16_t* C, int 
     }
     if (p.accumulate) {
       float old[4];
-      widen4<DT>(*reinterpret_cast<const u32x2*>(dst), old);
+      widen4<DT>(pre_old ? *pre_old : *reinterpret_cast<const u32x2*>(dst), old);
 #pragma unroll
       for (int e = 0; e < 4; ++e) v[e] += old[e];
     }
@@ -348,8 +355,13 @@ __device__ __forceinline__ void finish_tile(const GemmParams& p, f32x16 (&acc)[F
 // as a 64-deep stage above) behind ONE barrier: the small tiles, whose MMA
 // waves issue only a few MFMAs per 64 k, then meet at a barrier PL times less
 // often for the same bytes in flight.
+//
+// With EW (unsplit launches whose epilogue adds a residual) each thread loads
+// its residual words before the main loop (see `pre` below); other launches
+// run the EW = false build, which carries none of that code (the extra
+// registers and branches cost the plain qkv launch 0.7 us).
 template <int DT, int BM, int BN, int S, int EPI, int KG, int PW, int CV = 0, int WGN = 2,
-          int PL = 1, int WGM = 2>
+          int PL = 1, int WGM = 2, bool EW = false>
 __global__ void __launch_bounds__(64 * (WGM * WGN * KG + PW)) gemm_dma_kernel(const GemmParams p) {
   // WGM waves along m within a group (WGN along n)
   constexpr int GW = WGM * WGN;              // MMA waves per k group
@@ -405,6 +417,29 @@ __global__ void __launch_bounds__(64 * (WGM * WGN * KG + PW)) gemm_dma_kernel(co
   const int kbeg = split * p.kchunk;
   const int kend = min(p.K, kbeg + p.kchunk);
   const int nk = (kend - kbeg + SK - 1) / SK;
+
+  // The residual words of this thread's epilogue groups (the same thread ->
+  // group map as the store loop below), loaded here, before the ring's first
+  // DMA: they arrive while the main loop runs.  Read after the loop they
+  // added their latency to every launch (the 64 x 64 store phase: 1.1 us
+  // with a residual against 0.44 us without).  A producer wave's words are
+  // older than its DMA loads, so the loop's vmcnt waits, which count only
+  // the DMA behind them, complete them too.  Single-pass epilogues (EP = 1)
+  // with up to 12 groups per thread; the bias (one small, cached vector) is
+  // still read in the epilogue.
+  constexpr int EGPR = BN / 4;
+  constexpr int EIT = (BM * EGPR + NTH - 1) / NTH;
+  constexpr bool PRE = EW && EP == 1 && EPI != EPI_SILU && EIT <= 12;
+  u32x2 pre[PRE ? EIT : 1];
+  if constexpr (PRE) {
+#pragma unroll
+    for (int it = 0; it < EIT; ++it) {
+      const int idx = it * NTH + tid;
+      const int m = m0 + idx / EGPR, n = tn * BN + (idx % EGPR) * 4;
+      if ((BM * EGPR % NTH == 0 || idx < BM * EGPR) && m < p.M && n < p.N)
+        pre[it] = *reinterpret_cast<const u32x2*>(C + (int64_t)m * p.ldc + n);
+    }
+  }
 
   // Per-lane byte offsets at k = 0 of the row chunk this lane fetches: lane l
   // of DMA instruction j fills LDS row r = (NW*j + dwave)*8 + l/8 at physical
@@ -696,7 +731,10 @@ __global__ void __launch_bounds__(64 * (WGM * WGN * KG + PW)) gemm_dma_kernel(co
       }
       const float v[4] = {v4.x, v4.y, v4.z, v4.w};
       const float uu[4] = {u4.x, u4.y, u4.z, u4.w};
-      epilogue4<DT, EPI>(p, C, m, n, v, uu);
+      if constexpr (PRE)
+        epilogue4<DT, EPI>(p, C, m, n, v, uu, &pre[it]);
+      else
+        epilogue4<DT, EPI>(p, C, m, n, v, uu);
     }
   }
   if (pf_on) {
@@ -884,8 +922,19 @@ template <int DT, int BM, int BN, int S, int EPI, int KG, int PW, int CV = 0, in
 hipError_t launch_dma(const Plan& plan, const GemmParams& p, int batch, hipStream_t s,
                       const Stamps& ts) {
   const unsigned units = (unsigned)(plan.tiles_m * plan.tiles_n * plan.splits);
-  return launch_kernel(gemm_dma_kernel<DT, BM, BN, S, EPI, KG, PW, CV, WGN, PL, WGM>,
-                       dim3(units, (unsigned)batch), dim3(64 * (WGM * WGN * KG + PW)), s, ts, p);
+  const dim3 grid(units, (unsigned)batch), block(64 * (WGM * WGN * KG + PW));
+  // the EW build only where a residual exists and the kernel can hold it
+  constexpr int EP = BM * (BN + 4) * 4 <= S * (BM + BN) * 128 * PL ? 1 : 2;
+  constexpr int NTH = 64 * (WGM * WGN * KG + PW);
+  constexpr bool EW_OK =
+      CV == 0 && EPI != EPI_SILU && EP == 1 && (BM * BN / 4 + NTH - 1) / NTH <= 12;
+  if constexpr (EW_OK) {
+    if (plan.splits == 1 && p.accumulate)
+      return launch_kernel(gemm_dma_kernel<DT, BM, BN, S, EPI, KG, PW, CV, WGN, PL, WGM, true>,
+                           grid, block, s, ts, p);
+  }
+  return launch_kernel(gemm_dma_kernel<DT, BM, BN, S, EPI, KG, PW, CV, WGN, PL, WGM, false>, grid,
+                       block, s, ts, p);
 }
 
 template <int DT, int EPI>
