@@ -676,6 +676,49 @@ def bench_encoder(pkg, host, ctx, m, warmup, steps):
     return ev_ms, wall_ms, sites, flops
 
 
+def vs_hipblaslt(pkg, ctx, launches):
+    """The decoder's four projections at M = 1024 (config 3) and M = 4352 (the
+    300 s prefill), f16, warm weights (one W), `launches` back-to-back launches
+    each: first through qa_linear, then through torch's f16 GEMM (hipBLASLt on
+    this image): `addmm_` (beta = 1) where qa_linear adds the residual, a plain
+    `mm` for gate|up, which gets no SiLU.up epilogue in the library (its output
+    is twice as wide).  Only launches: the durations come from a kernel trace
+    of this run (rocprofv3 --kernel-trace), in the order returned."""
+    import torch
+    shapes = []
+    for m in (1024, 4352):
+        shapes += [(f"qkv/{m}", m, DEC["q_dim"] + 2 * DEC["kv_dim"], DEC["hidden"], 0),
+                   (f"o/{m}", m, DEC["hidden"], DEC["q_dim"], 1),
+                   (f"gu/{m}", m, 2 * DEC["inter"], DEC["hidden"], 2),
+                   (f"down/{m}", m, DEC["hidden"], DEC["inter"], 1)]
+    order = []
+    for name, m, n, k, fl in shapes:
+        rng = np.random.default_rng(0)
+        a = rng.standard_normal((m, k)).astype(np.float16)
+        w = (0.02 * rng.standard_normal((n, k))).astype(np.float16)
+        nout = n // 2 if fl == 2 else n
+        c = rng.standard_normal((m, nout)).astype(np.float16)
+        da, dw, dc = (ctx.to_device(x.view(np.uint16)) for x in (a, w, c))
+        flags = {0: 0, 1: pkg.ACCUMULATE, 2: pkg.EPI_SILU_MUL}[fl]
+        d = pkg.linear_desc(pkg.F16, m, n, k, da, dw, dc, flags=flags, ldc=nout)
+        for _ in range(launches):
+            ctx.linear(d)
+        ctx.sync()
+        for b in (da, dw, dc):
+            b.free()
+        ta, tw = torch.from_numpy(a).cuda(), torch.from_numpy(w).cuda()
+        tc = torch.from_numpy(c if fl != 2 else np.zeros((m, n), np.float16)).cuda()
+        torch.cuda.synchronize()
+        for _ in range(launches):
+            if fl == 1:
+                tc.addmm_(ta, tw.t())
+            else:
+                torch.mm(ta, tw.t(), out=tc)
+        torch.cuda.synchronize()
+        order.append(dict(shape=name, m=m, n=n, k=k, launches=launches))
+    return {"vs_hipblaslt": order, "blas": str(torch.backends.cuda.preferred_blas_library())}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -700,6 +743,10 @@ def main():
                          "graph replay, as a table of medians (one JSON line)")
     ap.add_argument("--warm", action="store_true",
                     help="with --site: repeat layer 0's (or config 1's first) W instead of cycling")
+    ap.add_argument("--vs-hipblaslt", action="store_true",
+                    help="only launch the decoder projections at M = 1024 and 4352 through "
+                         "qa_linear, then through torch's f16 GEMM (hipBLASLt), --launches each, "
+                         "for a kernel trace")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -709,6 +756,10 @@ def main():
 
     if args.phase_stamps:
         os.environ["QA_BUILD"] = "stamps"  # before the package loads its libraries
+    if args.vs_hipblaslt:
+        # torch's own HIP runtime and BLAS libraries first: loaded after this
+        # package's, torch's hipBLASLt / rocBLAS handles fail to initialise
+        import torch  # noqa: F401
     import __graft_entry__ as entry
 
     pkg = entry.load_package()
@@ -728,6 +779,11 @@ def main():
                 ms = ms[0::2] + ms[1::2]
             print(json.dumps({"site": args.site, "warm": args.warm, "weight_sets": len(descs),
                               "flops_per_launch": flops, "per_launch": dist(ms)}), flush=True)
+        return
+
+    if args.vs_hipblaslt:
+        with pkg.Context(0) as ctx:
+            print(json.dumps(vs_hipblaslt(pkg, ctx, args.launches)), flush=True)
         return
 
     if args.phase_stamps:
