@@ -216,7 +216,8 @@ __device__ __forceinline__ void widen4(u32x2 w, float* v) {
 template <int DT, int EPI>
 __device__ __forceinline__ void epilogue4(const GemmParams& p, uint16_t* C, int m, int n,
                                           const float* v_in, const float* u_in,
-                                          const u32x2* pre_old = nullptr) {
+                                          const u32x2* pre_old = nullptr,
+                                          const u32x2* pre_bias = nullptr) {
   uint16_t* dst = C + (int64_t)m * p.ldc + n;
   float v[4];
   if constexpr (EPI == EPI_SILU) {
@@ -236,7 +237,7 @@ __device__ __forceinline__ void epilogue4(const GemmParams& p, uint16_t* C, int 
         for (int e = 0; e < 4; ++e) v[e] += b;
       } else {
         float b[4];
-        widen4<DT>(*reinterpret_cast<const u32x2*>(p.bias + n), b);
+        widen4<DT>(pre_bias ? *pre_bias : *reinterpret_cast<const u32x2*>(p.bias + n), b);
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] += b[e];
       }
@@ -356,12 +357,23 @@ __device__ __forceinline__ void finish_tile(const GemmParams& p, f32x16 (&acc)[F
 // waves issue only a few MFMAs per 64 k, then meet at a barrier PL times less
 // often for the same bytes in flight.
 //
-// With EW (unsplit launches whose epilogue adds a residual) each thread loads
-// its residual words before the main loop (see `pre` below); other launches
-// run the EW = false build, which carries none of that code (the extra
-// registers and branches cost the plain qkv launch 0.7 us).
+// EW is a mask of epilogue words each thread loads before the main loop, in
+// unsplit launches that have them: EW_RESIDUAL the residual (`pre` below),
+// EW_BIAS the column bias (`bpre`).  Other launches run the EW = 0 build,
+// which carries none of that code (the extra registers and branches cost the
+// plain qkv launch 0.7 us).
+constexpr int EW_RESIDUAL = 1, EW_BIAS = 2;
+
+// Smallest p >= 1 with p * nth a multiple of gpr: the store loop's thread ->
+// column-group map repeats every p iterations.
+constexpr int group_period(int nth, int gpr) {
+  int q = 1;
+  while ((q * nth) % gpr) ++q;
+  return q;
+}
+
 template <int DT, int BM, int BN, int S, int EPI, int KG, int PW, int CV = 0, int WGN = 2,
-          int PL = 1, int WGM = 2, bool EW = false>
+          int PL = 1, int WGM = 2, int EW = 0>
 __global__ void __launch_bounds__(64 * (WGM * WGN * KG + PW)) gemm_dma_kernel(const GemmParams p) {
   // WGM waves along m within a group (WGN along n)
   constexpr int GW = WGM * WGN;              // MMA waves per k group
@@ -429,7 +441,7 @@ __global__ void __launch_bounds__(64 * (WGM * WGN * KG + PW)) gemm_dma_kernel(co
   // still read in the epilogue.
   constexpr int EGPR = BN / 4;
   constexpr int EIT = (BM * EGPR + NTH - 1) / NTH;
-  constexpr bool PRE = EW && EP == 1 && EPI != EPI_SILU && EIT <= 12;
+  constexpr bool PRE = (EW & EW_RESIDUAL) && EP == 1 && EPI != EPI_SILU && EIT <= 12;
   u32x2 pre[PRE ? EIT : 1];
   if constexpr (PRE) {
 #pragma unroll
@@ -438,6 +450,23 @@ __global__ void __launch_bounds__(64 * (WGM * WGN * KG + PW)) gemm_dma_kernel(co
       const int m = m0 + idx / EGPR, n = tn * BN + (idx % EGPR) * 4;
       if ((BM * EGPR % NTH == 0 || idx < BM * EGPR) && m < p.M && n < p.N)
         pre[it] = *reinterpret_cast<const u32x2*>(C + (int64_t)m * p.ldc + n);
+    }
+  }
+  // The column bias of the same groups, also loaded here.  A thread's groups
+  // repeat their columns every BPER store iterations (one to three words
+  // for these tiles).  Read in the epilogue, each group's bias word came after
+  // the previous groups' stores, and since vmcnt counts stores too, waiting
+  // for it waited for those stores to be acknowledged: one write-through
+  // round trip per group (the tower's 256 x 256 GELU launch: 15 us of stores
+  // with a bias).
+  constexpr bool BPRE = (EW & EW_BIAS) && EPI != EPI_SILU;
+  constexpr int BPER = BPRE ? group_period(NTH, EGPR) : 1;
+  u32x2 bpre[BPER];
+  if constexpr (BPRE) {
+#pragma unroll
+    for (int j = 0; j < BPER; ++j) {
+      const int n = tn * BN + ((j * NTH + tid) % EGPR) * 4;
+      if (n < p.N) bpre[j] = *reinterpret_cast<const u32x2*>(p.bias + n);
     }
   }
 
@@ -731,10 +760,12 @@ __global__ void __launch_bounds__(64 * (WGM * WGN * KG + PW)) gemm_dma_kernel(co
       }
       const float v[4] = {v4.x, v4.y, v4.z, v4.w};
       const float uu[4] = {u4.x, u4.y, u4.z, u4.w};
+      const u32x2* bw = nullptr;
+      if constexpr (BPRE) bw = &bpre[it % BPER];
       if constexpr (PRE)
-        epilogue4<DT, EPI>(p, C, m, n, v, uu, &pre[it]);
+        epilogue4<DT, EPI>(p, C, m, n, v, uu, &pre[it], bw);
       else
-        epilogue4<DT, EPI>(p, C, m, n, v, uu);
+        epilogue4<DT, EPI>(p, C, m, n, v, uu, nullptr, bw);
     }
   }
   if (pf_on) {
@@ -923,17 +954,31 @@ hipError_t launch_dma(const Plan& plan, const GemmParams& p, int batch, hipStrea
                       const Stamps& ts) {
   const unsigned units = (unsigned)(plan.tiles_m * plan.tiles_n * plan.splits);
   const dim3 grid(units, (unsigned)batch), block(64 * (WGM * WGN * KG + PW));
-  // the EW build only where a residual exists and the kernel can hold it
+  // The preloading builds only where their words exist (unsplit launches: a
+  // split launch's epilogue runs in the reduce kernel): the residual where
+  // the kernel can hold it, the column bias on every non-SiLU tile.
   constexpr int EP = BM * (BN + 4) * 4 <= S * (BM + BN) * 128 * PL ? 1 : 2;
   constexpr int NTH = 64 * (WGM * WGN * KG + PW);
-  constexpr bool EW_OK =
-      CV == 0 && EPI != EPI_SILU && EP == 1 && (BM * BN / 4 + NTH - 1) / NTH <= 12;
-  if constexpr (EW_OK) {
-    if (plan.splits == 1 && p.accumulate)
-      return launch_kernel(gemm_dma_kernel<DT, BM, BN, S, EPI, KG, PW, CV, WGN, PL, WGM, true>,
+  constexpr bool RES_OK =
+      CV == 0 && EPI == EPI_PLAIN && EP == 1 && (BM * BN / 4 + NTH - 1) / NTH <= 12;
+  const bool res = RES_OK && plan.splits == 1 && p.accumulate;
+  const bool bw = EPI != EPI_SILU && plan.splits == 1 && p.bias && !p.bias_rows;
+  if constexpr (EPI != EPI_SILU) {
+    if constexpr (RES_OK) {
+      if (res && bw)
+        return launch_kernel(
+            gemm_dma_kernel<DT, BM, BN, S, EPI, KG, PW, CV, WGN, PL, WGM, EW_RESIDUAL | EW_BIAS>,
+            grid, block, s, ts, p);
+      if (res)
+        return launch_kernel(
+            gemm_dma_kernel<DT, BM, BN, S, EPI, KG, PW, CV, WGN, PL, WGM, EW_RESIDUAL>, grid,
+            block, s, ts, p);
+    }
+    if (bw)
+      return launch_kernel(gemm_dma_kernel<DT, BM, BN, S, EPI, KG, PW, CV, WGN, PL, WGM, EW_BIAS>,
                            grid, block, s, ts, p);
   }
-  return launch_kernel(gemm_dma_kernel<DT, BM, BN, S, EPI, KG, PW, CV, WGN, PL, WGM, false>, grid,
+  return launch_kernel(gemm_dma_kernel<DT, BM, BN, S, EPI, KG, PW, CV, WGN, PL, WGM, 0>, grid,
                        block, s, ts, p);
 }
 
