@@ -243,3 +243,19 @@ def logits_gate(orc, dtype, got_rows, got_logits, want_rows, top_idx, top_logits
     got = np.take_along_axis(np.asarray(got_logits, np.float64), top_idx, axis=1)
     use = np.abs(got - top_logits) / bound
     return bool(np.isfinite(got).all() and (use <= 1.0).all()), float(use.max())
+
+
+def discriminating_head(orc, dtype, rows_bits, norm_w, score, k=4):
+    """A score head under which the slots' classes differ: `score` with the k
+    leading principal directions of the slots' folded rows (head_fold of
+    rows_bits) projected out of every label's row.  At random init those
+    directions carry what every <timestamp> row shares (its embedding and
+    what the layers make of it), which gives every slot the same class under
+    the random head; what is left follows how the slots differ.  It gives the
+    class gates something to decide.  f32, like the checkpoint's head."""
+    pos = np.arange(rows_bits.shape[0])
+    y = orc.head_fold(dtype, rows_bits, pos, norm_w, EPS).astype(np.float64)
+    _, _, vt = np.linalg.svd(y, full_matrices=False)
+    s = np.asarray(score, np.float64)
+    return (s - (s @ vt[:k].T) @ vt[:k]).astype(np.float32)
+

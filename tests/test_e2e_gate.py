@@ -98,3 +98,32 @@ def test_logits_gate_rejects_a_shifted_row(orc, tiny):
     ok, use = logits_gate(orc, 0, rows, logits, rows, arr["chain16_top_idx"],
                           arr["chain16_top_logits"], w["norm_w"], w["score"])
     assert ok, use
+
+
+def test_discriminating_head_makes_the_classes_decide(pkg, orc):
+    """On the 300 s fixture's rows (tests/golden/e2e_300s.npz) the random
+    head gives every slot the same class, so classes read from each slot's
+    neighbour (a wrong timestamp position) equal the right ones and a class
+    comparison cannot see the mistake.  Under chains.discriminating_head the
+    classes differ across slots and the same mistake changes most of them
+    (82% of the 240; a word's two slots sit side by side and often agree)."""
+    from chains import EPS, discriminating_head
+    from qwen3_aligner_wgpu_amd import synthetic as syn
+    path = os.path.join(HERE, "golden", "e2e_300s")
+    c = json.load(open(path + ".json"))["config"]
+    rows = np.load(path + ".npz")["chain16_rows"]
+    dt = c["dtype"]
+    w = syn.aligner_weights(dt, 0, 0, c["seed"])  # embed / norm / head only
+    pos = np.arange(rows.shape[0])
+
+    def classes(score, r):
+        return orc.timestamp_head(dt, r, pos, w["norm_w"], EPS, score)[1]
+
+    shifted = np.roll(rows, 1, axis=0)
+    plain = classes(w["score"], rows)
+    assert np.unique(plain).size == 1
+    assert np.array_equal(classes(w["score"], shifted), plain)  # the mistake is invisible
+    head2 = discriminating_head(orc, dt, rows, w["norm_w"], w["score"])
+    good = classes(head2, rows)
+    assert np.unique(good).size >= rows.shape[0] // 2
+    assert (classes(head2, shifted) != good).mean() > 0.5  # neighbours often share a class

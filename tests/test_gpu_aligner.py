@@ -32,7 +32,11 @@ Gates:
     forward (its f32 tower).  With random-init weights the <timestamp>
     embedding dominates those rows, so every slot picks the same class: the
     classes alone would not tell a correct forward from a wrong one, the rows
-    and logits do.
+    and logits do;
+  * the head stage again with a head whose classes differ by slot
+    (chains.discriminating_head: the random head with the rows' shared
+    directions projected out), rerun on the same aligner: logits within the
+    f32 bound, every class a maximum within it, classes varied.
 """
 from __future__ import annotations
 
@@ -58,7 +62,10 @@ def _inputs(seconds, n_words, seed):
     return x, words
 
 
-def _run(pkg, ctx, dtype, w, x, words, max_rows):
+def _run(pkg, ctx, dtype, w, x, words, max_rows, heads=()):
+    """The forward with w's head, then once more per extra score head in
+    `heads` (loaded into the same aligner): out["extra"][i] holds that
+    forward's classes, logits and final rows."""
     from qwen3_aligner_wgpu_amd import synthetic as syn
     al, enc, dec = syn.build_aligner(pkg, ctx, dtype, w, x.size / 16000 + 0.01, max_rows)
     try:
@@ -67,7 +74,12 @@ def _run(pkg, ctx, dtype, w, x, words, max_rows):
         raw, fixed = al.result()
         out = dict(info=info, raw=raw, fixed=fixed, classes=al.read("classes"),
                    logits=al.read("logits"), ids=al.read("ids"), src=al.read("src"),
-                   ts=al.read("ts_pos"), h=dec.read("h", info["seq"]))
+                   ts=al.read("ts_pos"), h=dec.read("h", info["seq"]), extra=[])
+        for score in heads:
+            al.load_head(w["norm_w"], score)
+            al.forward()
+            out["extra"].append(dict(classes=al.read("classes"), logits=al.read("logits"),
+                                     h=dec.read("h", info["seq"])))
     finally:
         al.close()
         enc.close()
@@ -79,17 +91,52 @@ def _clear(gap, rms):
     return np.asarray(gap) > NEAR_TIE * np.asarray(rms)
 
 
+def _discriminating_gate(orc, dtype, g, e, ts, norm_w, score, min_distinct):
+    """The forward `e`, run with a discriminating head (chains.discriminating_head)
+    loaded into the same aligner: its final rows equal the first forward's
+    (only the head changed); its logits are within the f32 head's error bound
+    of the oracle head's (f64) on those rows; at every slot its class is a
+    maximum of the exact logits to within that bound (the chosen label's
+    exact logit at least the best one's less both labels' bounds), and equals
+    the oracle's class wherever the best two logits are apart by more than
+    twice the bound; and the classes differ across slots (at least
+    min_distinct), so this head-stage gate decides something, which the
+    random head, with one class at every slot, does not.  The head's classes
+    are not compared across two forwards: with the shared directions
+    projected out they follow the rows' smallest differences, and two correct
+    oracle forwards of the 300 s config (16-bit and f32 tower, 1.3e-3
+    relative RMS apart) agree at fewer than half of the slots under it."""
+    rows = e["h"][ts]
+    assert np.array_equal(e["h"], g["h"])
+    hl, hc = orc.timestamp_head(dtype, rows, np.arange(ts.size), norm_w, EPS, score)
+    y = orc.head_fold(dtype, rows, np.arange(ts.size), norm_w, EPS).astype(np.float64)
+    bound = (2 * y.shape[1] + 64) * 2.0 ** -24 * (np.abs(y) @ np.abs(score.astype(np.float64)).T)
+    assert (np.abs(e["logits"] - hl) <= bound).all()
+    r = np.arange(ts.size)
+    cls = e["classes"]
+    assert (hl[r, cls] >= hl[r, hc] - bound[r, cls] - bound[r, hc]).all()
+    top2 = np.sort(hl, axis=1)[:, -2:]
+    sure = top2[:, 1] - top2[:, 0] > 2 * bound.max(axis=1)
+    assert np.array_equal(cls[sure], hc[sure])
+    distinct = np.unique(cls).size
+    print(f"discriminating head: {distinct} distinct classes over {ts.size} slots, equal to the "
+          f"oracle head's at {(cls == hc).sum()} ({sure.sum()} outside twice the f32 bound)")
+    assert distinct >= min_distinct, distinct
+
 
 @pytest.mark.parametrize("dtype,seconds,n_words,layers", [(F16, 7.37, 16, (2, 3)),
                                                           (BF16, 4.0, 9, (1, 2))],
                          ids=["f16-7s", "bf16-4s"])
 def test_aligner_against_oracle_chain(ctx, pkg, orc, dtype, seconds, n_words, layers):
     from qwen3_aligner_wgpu_amd import synthetic as syn
+    from chains import discriminating_head
     w = syn.aligner_weights(dtype, *layers, seed=7)
     x, words = _inputs(seconds, n_words, 11)
-    g = _run(pkg, ctx, dtype, w, x, words, 512)
     r = oracle_aligner(orc, dtype, w, x, words, pkg.mel_filterbank(),
                        lambda n: pkg.rope_tables(n, 128, 1e6, dtype))
+    _, _, ts0 = assemble(r["n_audio"], words)
+    head2 = discriminating_head(orc, dtype, r["h"][ts0], w["norm_w"], w["score"])
+    g = _run(pkg, ctx, dtype, w, x, words, 512, heads=[head2])
     # the assembled input
     assert g["info"]["n_audio"] == r["n_audio"] and g["info"]["seq"] == r["ids"].size
     ids, src, ts = assemble(r["n_audio"], words)
@@ -118,6 +165,9 @@ def test_aligner_against_oracle_chain(ctx, pkg, orc, dtype, seconds, n_words, la
           f"({clear.sum()} with a clear margin)")
     assert np.array_equal(g["raw"], (g["classes"] * 80).astype(np.int64))
     assert list(g["fixed"]) == orc.fix_timestamps(list(g["raw"]))
+    # a head whose classes differ by slot
+    _discriminating_gate(orc, dtype, g, g["extra"][0], ts, w["norm_w"], head2,
+                         min_distinct=ts.size // 4)
 
 
 def test_aligner_e2e_300s_against_fixture(ctx, pkg, orc):
@@ -136,7 +186,10 @@ def test_aligner_e2e_300s_against_fixture(ctx, pkg, orc):
       * the classes identical at every slot with a clear oracle margin;
       * against the reference CPU path's forward (f32 tower, cpu_ref): the
         rows within twice the oracle chains' distance, and the classes
-        identical at clear slots."""
+        identical at clear slots;
+      * the head stage once more under a discriminating head built from the
+        fixture's rows (_discriminating_gate): the random head gives every
+        slot one class, this one about 180 over the 240 slots."""
     from qwen3_aligner_wgpu_amd import synthetic as syn
     from chains import logits_gate, rows_gate
     path = os.path.join(HERE, "golden", "e2e_300s")
@@ -150,7 +203,9 @@ def test_aligner_e2e_300s_against_fixture(ctx, pkg, orc):
     dg = lambda a: hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()[:16]  # noqa: E731
     assert dg(w["embed"]) == gold["digests"]["embed"] and dg(w["score"]) == gold["digests"]["score"]
     same_audio = dg(x) == gold["digests"]["samples"]
-    g = _run(pkg, ctx, c["dtype"], w, x, words, 4352)
+    from chains import discriminating_head
+    head2 = discriminating_head(orc, c["dtype"], arr["chain16_rows"], w["norm_w"], w["score"])
+    g = _run(pkg, ctx, c["dtype"], w, x, words, 4352, heads=[head2])
     assert g["info"]["seq"] == gold["seq"] and g["info"]["n_audio"] == gold["n_audio"]
     assert dg(g["ids"]) == gold["digests"]["ids"]
     assert list(g["ts"]) == gold["ts"]
@@ -180,6 +235,10 @@ def test_aligner_e2e_300s_against_fixture(ctx, pkg, orc):
           f"{same_ref.sum()}/{want_ref.size} slots ({clear_ref.sum()} clear)")
     assert st_ref["rel_rms"] <= 2 * drift["rel_rms"], (st_ref, drift)
     assert same_ref[clear_ref].all(), np.nonzero(~same_ref & clear_ref)
+    # every slot's class above is the same one (random init): the head stage
+    # again under a head whose classes differ by slot
+    _discriminating_gate(orc, c["dtype"], g, g["extra"][0], g["ts"], w["norm_w"], head2,
+                         min_distinct=g["ts"].size // 4)
 
 
 def test_failed_prepare_forgets_the_previous_clip(ctx, pkg):
