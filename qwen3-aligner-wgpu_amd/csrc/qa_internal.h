@@ -55,15 +55,22 @@ inline TileShape tile_shape(int cfg) {
 // libm's erff (src/audio_encoder.rs:196-202).
 //   erf(a) = 1 - P(t) e^{-a^2},  t = 1 / (1 + 0.3275911 a),  a >= 0;
 // for x < 0 the factor 1 + erf(x / sqrt 2) = P(t) e^{-a^2} is formed directly,
-// without cancelling against 1.
+// without cancelling against 1.  Arranged for the VALU (15 instructions, two
+// of them quarter-rate transcendentals, against 17): with q = P(t) e^{-a^2} / 2
+// (the coefficients halved, an exact scaling), gelu(x) = max(x, -0) - |x| q
+// for either sign (x - x q for x >= 0, x q for x < 0: no cancellation on the
+// negative side), one FMA that keeps a zero result's sign and propagates NaN;
+// 1/sqrt 2 folds into the reciprocal's FMA and the exponent's constant.
+// (+inf gives NaN through inf * 0, where 0.5 x (2 - q) gave +inf; an f32 sum
+// of 16-bit products does not reach it.)
 __device__ __forceinline__ float gelu_erf(float x) {
-  const float a = fabsf(x) * 0.70710678118654752f;
-  const float t = __builtin_amdgcn_rcpf(1.0f + 0.3275911f * a);
-  const float poly =
-      ((((1.061405429f * t - 1.453152027f) * t + 1.421413741f) * t - 0.284496736f) * t +
-       0.254829592f) * t;
-  const float q = poly * __builtin_amdgcn_exp2f(-a * a * 1.44269504088896341f);  // 1 - erf(a)
-  return 0.5f * x * (x >= 0.0f ? 2.0f - q : q);
+  constexpr float h = 0.5f;
+  const float ax = fabsf(x);
+  const float t = __builtin_amdgcn_rcpf(fmaf(ax, 0.3275911f * 0.70710678118654752f, 1.0f));
+  const float e = __builtin_amdgcn_exp2f(x * x * (-0.5f * 1.44269504088896341f));  // e^{-a^2}
+  const float p = (((h * 1.061405429f * t - h * 1.453152027f) * t + h * 1.421413741f) * t -
+                   h * 0.284496736f) * t + h * 0.254829592f;
+  return fmaf(-ax, p * t * e, fmaxf(x, -0.0f));
 }
 
 struct GemmParams {
