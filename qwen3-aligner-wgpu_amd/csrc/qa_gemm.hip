@@ -113,11 +113,10 @@ struct Fmt<QA_BF16> {
 __device__ __forceinline__ int swz(int row) { return (row >> 1) & 7; }
 
 __device__ __forceinline__ int xcd_remap(int b, int n) {
-  constexpr int X = 8;  // XCDs per MI355X
-  const int full = n - n % X;
-  if (b >= full) return b;
-  const int per = full / X;
-  return (b % X) * per + b / X;
+  constexpr unsigned X = 8;  // XCDs per MI355X
+  const unsigned ub = (unsigned)b, full = (unsigned)n - (unsigned)n % X;
+  if (ub >= full) return b;
+  return (int)((ub % X) * (full / X) + ub / X);
 }
 
 // Block -> (tile m, tile n, k split).  Workgroups are dealt round-robin over
@@ -133,14 +132,15 @@ __device__ __forceinline__ int xcd_remap(int b, int n) {
 __device__ __forceinline__ void tile_of(const GemmParams& p, int b, int& tm, int& tn,
                                         int& split) {
   const int u = xcd_remap(b, p.tiles_m * p.tiles_n * p.splits);
-  split = u % p.splits;
-  const int t = u / p.splits;
+  const int t = fastdiv(u, p.fd_split);
+  split = u - t * p.splits;
   const int g = p.group_m;
-  const int band = t / (g * p.tiles_n);
+  const int band = fastdiv(t, p.fd_band);
   const int i = t - band * g * p.tiles_n;
-  const int rows = min(g, p.tiles_m - band * g);
-  tm = band * g + i % rows;
-  tn = i / rows;
+  const bool last = (band + 1) * g > p.tiles_m;  // a short last band
+  const int rows = last ? p.tiles_m - band * g : g;
+  tn = fastdiv(i, last ? p.fd_last : p.fd_rows);
+  tm = band * g + (i - tn * rows);
 }
 
 // s_waitcnt vmcnt(N) leaving expcnt / lgkmcnt unconstrained (gfx9 encoding).
@@ -1070,12 +1070,15 @@ static int g_stamp_next = 0;  // the next launch's record slot
 hipError_t launch_gemm(int dtype, const Plan& plan, const GemmParams& p_in, int batch,
                        hipStream_t stream, hipEvent_t t0, hipEvent_t t1) {
   const Stamps ts{t0, t1};
-#ifdef QA_PHASE_STAMPS
   GemmParams p = p_in;
+  const int g = p.group_m, bands = (p.tiles_m + g - 1) / g;
+  p.fd_split = fastdiv_make((uint32_t)p.splits);
+  p.fd_band = fastdiv_make((uint32_t)(g * p.tiles_n));
+  p.fd_rows = fastdiv_make((uint32_t)g);
+  p.fd_last = fastdiv_make((uint32_t)(p.tiles_m - (bands - 1) * g));
+#ifdef QA_PHASE_STAMPS
   p.stamp_slot = g_stamp_next;
   g_stamp_next = (g_stamp_next + 1) % kStampSlots;
-#else
-  const GemmParams& p = p_in;
 #endif
   if (dtype == QA_BF16) return launch_dt<QA_BF16>(plan, p, batch, stream, ts);
   return launch_dt<QA_F16>(plan, p, batch, stream, ts);

@@ -48,6 +48,28 @@ inline TileShape tile_shape(int cfg) {
   }
 }
 
+// q = floor(n / d) for 0 <= n < 2^31 and 1 <= d < 2^31 as one 32 x 32 -> 64-bit
+// multiply and a shift (Granlund & Montgomery, "Division by invariant integers
+// using multiplication", PLDI 1994): with l = ceil(log2 d), p = 31 + l and
+// m = ceil(2^p / d) < 2^32, m d = 2^p + e with 0 <= e < d, so
+// n m / 2^p = n / d + n e / (d 2^p) where the second term is below
+// 2^31 / 2^p = 2^-l <= 1 / d, too small to reach the next integer.  The
+// kernels' tile enumeration divides block indices by per-launch constants;
+// hipcc's generic signed division of a run-time divisor is a float reciprocal,
+// a VALU -> SALU move and ~15 scalar corrections per quotient.
+struct FastDiv {
+  uint32_t m, p;
+};
+inline FastDiv fastdiv_make(uint32_t d) {
+  uint32_t l = 0;
+  while ((1ull << l) < d) ++l;
+  const uint32_t p = 31 + l;
+  return {(uint32_t)(((1ull << p) + d - 1) / d), p};
+}
+__device__ __forceinline__ int fastdiv(int n, FastDiv f) {
+  return (int)(((uint64_t)(uint32_t)n * f.m) >> f.p);
+}
+
 // Kernel parameters (passed by value).  Element units throughout.
 // erf-form GELU, 0.5 x (1 + erf(x / sqrt 2)), with erf from Abramowitz &
 // Stegun 7.1.26 (|error| <= 1.5e-7) on v_exp_f32 / v_rcp_f32: the form of the
@@ -89,6 +111,9 @@ struct GemmParams {
   int accumulate;        // add C_old before the rounding
   int bias_rows;         // bias indexed by output row (channel-major conv)
   int group_m;           // m-tiles per band of the tile enumeration (tile_of)
+  // divisions of tile_of by splits, band size group_m * tiles_n, a full band's
+  // height group_m and the last band's (launch_gemm fills them)
+  FastDiv fd_split, fd_band, fd_rows, fd_last;
   // implicit 3x3 / stride-2 / pad-1 convolution A operand (Plan::conv)
   int cv_c, cv_h, cv_w;  // input channels (multiple of 8, >= 64), height, width
   int cv_ho, cv_wo;      // output height, width
