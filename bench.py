@@ -407,11 +407,14 @@ def phase_stamps(pkg, host, ctx, warmup, steps):
     layers: qkv, o, gate|up, down), reduced per launch to medians over its
     blocks (us): gap from the previous launch's last block end, start skew
     (first to last block start), fill (start to ring stage 0 in), main loop,
-    park (accumulators to LDS), stores (first store to block end), span."""
+    park (accumulators to LDS), stores (first store to block end), span; and
+    the fill split at the first DMA-issuing thread's prologue points: kernel
+    arguments in, tile enumeration, issue of the first ring stages, wait for
+    stage 0."""
     L = pkg.lib()
-    L.qa_phase_stamps_read.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
-    slots, blocks = ctypes.c_int(), ctypes.c_int()
-    L.qa_phase_stamps_read(None, ctypes.byref(slots), ctypes.byref(blocks))
+    L.qa_phase_stamps_read.argtypes = [ctypes.c_void_p] * 4
+    slots, blocks, words = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    L.qa_phase_stamps_read(None, ctypes.byref(slots), ctypes.byref(blocks), ctypes.byref(words))
     m = 1024
     dec = host.DecoderLinears(ctx, pkg.F16, DEC["layers"], m, DEC["hidden"], DEC["q_dim"],
                               DEC["kv_dim"], DEC["inter"])
@@ -425,8 +428,8 @@ def phase_stamps(pkg, host, ctx, warmup, steps):
     dec.time(m, max(1, warmup), 1, use_graph=True)  # capture; the records' slots are fixed then
     pkg.check(L.qa_phase_stamps_clear())
     ms, _ = dec.time(m, 0, max(1, steps), use_graph=True)
-    rec = np.zeros((slots.value, blocks.value, 8), np.uint64)
-    pkg.check(L.qa_phase_stamps_read(rec.ctypes.data, None, None))
+    rec = np.zeros((slots.value, blocks.value, words.value), np.uint64)
+    pkg.check(L.qa_phase_stamps_read(rec.ctypes.data, None, None, None))
     dec.close()
     names = {(4096, 1024): "qkv", (1024, 2048): "o", (6144, 1024): "gu", (1024, 3072): "down"}
     launches = []
@@ -445,7 +448,9 @@ def phase_stamps(pkg, host, ctx, warmup, steps):
                     "start_skew": round(int(t[0].max() - t[0].min()) / 100.0, 2),
                     "fill": med(t[1] - t[0]), "loop": med(t[2] - t[1]), "park": med(t[3] - t[2]),
                     "stores": med(t[4] - t[3]),
-                    "span": round(int(t[4].max() - t[0].min()) / 100.0, 2)})
+                    "span": round(int(t[4].max() - t[0].min()) / 100.0, 2),
+                    "fill_args": med(r[:, 8] - t[0]), "fill_tile_enum": med(r[:, 9] - r[:, 8]),
+                    "fill_issue": med(r[:, 10] - r[:, 9]), "fill_stage0_wait": med(t[1] - r[:, 10])})
         prev_end = int(t[4].max())
     return {"phase_stamps_config3": out, "step_ms": round(ms, 4),
             "note": "measurement build (-DQA_PHASE_STAMPS); medians over blocks, us; the last "

@@ -53,9 +53,11 @@ namespace qa {
 // Measurement build only (make stamps): every block of a gemm_dma_kernel
 // launch records s_memrealtime (100 MHz) at its start, when ring stage 0 is
 // in (after the first barrier), after the main loop, after the park (the
-// first store) and at its end, plus its CU id and the launch's N and K, in
-// record slot p.stamp_slot; the host cycles the slots launch by launch.
-constexpr int kStampSlots = 8, kStampBlocks = 2048, kStampWords = 8;
+// first store) and at its end, plus its CU id and the launch's N and K, and
+// three points of its first DMA-issuing thread's prologue (kernel arguments
+// in, tile enumeration done, the first S ring stages issued), in record slot
+// p.stamp_slot; the host cycles the slots launch by launch.
+constexpr int kStampSlots = 8, kStampBlocks = 2048, kStampWords = 12;
 __device__ unsigned long long stamp_log[kStampSlots * kStampBlocks * kStampWords];
 #endif
 
@@ -413,9 +415,25 @@ __global__ void __launch_bounds__(64 * (WGM * WGN * KG + PW)) gemm_dma_kernel(co
 
 #ifdef QA_PHASE_STAMPS
   unsigned long long st[5] = {__builtin_amdgcn_s_memrealtime(), 0, 0, 0, 0};
+  // prologue points of the first DMA-issuing thread; the empty asm statements
+  // make each stamp wait for the value it follows
+  __shared__ unsigned long long pro[3];
+  const int pro_tid = PW > 0 ? NMW * 64 : 0;
+  {
+    const int kv = p.K;
+    asm volatile("" ::"s"(kv));
+    if (tid == pro_tid) {
+      pro[0] = __builtin_amdgcn_s_memrealtime();
+      pro[2] = 0;
+    }
+  }
 #endif
   int tm, tn, split;
   tile_of(p, (int)blockIdx.x, tm, tn, split);
+#ifdef QA_PHASE_STAMPS
+  asm volatile("" ::"v"(tm), "v"(tn), "v"(split));
+  if (tid == pro_tid) pro[1] = __builtin_amdgcn_s_memrealtime();
+#endif
   const int64_t z = blockIdx.y;
   const uint16_t* A = p.a + z * p.bsa;
   const uint16_t* W = p.w + z * p.bsb;
@@ -615,6 +633,9 @@ __global__ void __launch_bounds__(64 * (WGM * WGN * KG + PW)) gemm_dma_kernel(co
 #pragma unroll
     for (int s = 0; s < S; ++s)
       if (s < nk) issue(s, s);
+#ifdef QA_PHASE_STAMPS
+    if (tid == pro_tid) pro[2] = __builtin_amdgcn_s_memrealtime();
+#endif
     if (S - 1 < nk)
       wait_vmcnt<(S - 1) * LPS>();
     else
@@ -640,6 +661,9 @@ __global__ void __launch_bounds__(64 * (WGM * WGN * KG + PW)) gemm_dma_kernel(co
 #pragma unroll
       for (int s = 0; s < S; ++s)
         if (s < nk) issue(s, s);
+#ifdef QA_PHASE_STAMPS
+      if (tid == pro_tid) pro[2] = __builtin_amdgcn_s_memrealtime();
+#endif
       if (S - 1 < nk)
         wait_vmcnt<(S - 1) * LPS>();
       else
@@ -782,6 +806,7 @@ __global__ void __launch_bounds__(64 * (WGM * WGN * KG + PW)) gemm_dma_kernel(co
     d[5] = (unsigned long long)__smid();
     d[6] = (unsigned long long)p.N;
     d[7] = (unsigned long long)p.K;
+    for (int i = 0; i < 3; ++i) d[8 + i] = pro[i];
   }
 #endif
 }
@@ -1087,11 +1112,14 @@ hipError_t launch_gemm(int dtype, const Plan& plan, const GemmParams& p_in, int 
 }  // namespace qa
 
 #ifdef QA_PHASE_STAMPS
-// The measurement build's stamp records: kStampSlots x kStampBlocks x 8
-// words (see stamp_log), copied to `out`; *slots, *blocks get the sizes.
-extern "C" int qa_phase_stamps_read(unsigned long long* out, int* slots, int* blocks) {
+// The measurement build's stamp records: kStampSlots x kStampBlocks x
+// kStampWords words (see stamp_log), copied to `out`; *slots, *blocks and
+// *words get the sizes.
+extern "C" int qa_phase_stamps_read(unsigned long long* out, int* slots, int* blocks,
+                                    int* words) {
   if (slots) *slots = qa::kStampSlots;
   if (blocks) *blocks = qa::kStampBlocks;
+  if (words) *words = qa::kStampWords;
   if (!out) return QA_OK;
   const hipError_t e = hipMemcpyFromSymbol(out, HIP_SYMBOL(qa::stamp_log), sizeof(qa::stamp_log));
   return e == hipSuccess ? QA_OK : QA_EDEVICE;
