@@ -1096,7 +1096,7 @@ hipError_t launch_gemm(int dtype, const Plan& plan, const GemmParams& p_in, int 
                        hipStream_t stream, hipEvent_t t0, hipEvent_t t1) {
   const Stamps ts{t0, t1};
   GemmParams p = p_in;
-  const int g = p.group_m, bands = (p.tiles_m + g - 1) / g;
+  const int g = p.group_m > 0 ? p.group_m : 1, bands = (p.tiles_m + g - 1) / g;
   p.fd_split = fastdiv_make((uint32_t)p.splits);
   p.fd_band = fastdiv_make((uint32_t)(g * p.tiles_n));
   p.fd_rows = fastdiv_make((uint32_t)g);

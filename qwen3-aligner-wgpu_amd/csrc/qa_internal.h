@@ -61,6 +61,7 @@ struct FastDiv {
   uint32_t m, p;
 };
 inline FastDiv fastdiv_make(uint32_t d) {
+  if (d == 0) return {0, 0};  // never divided by (no tiles, nothing launched)
   uint32_t l = 0;
   while ((1ull << l) < d) ++l;
   const uint32_t p = 31 + l;
