@@ -145,6 +145,15 @@ __device__ __forceinline__ void tile_of(const GemmParams& p, int b, int& tm, int
   tm = band * g + (i - tn * rows);
 }
 
+// A value the caller knows to be equal in every lane, as a scalar register.
+__device__ __forceinline__ int wave_uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// One 16-byte-per-lane DMA of a buffer into LDS (buffer_load_dwordx4 ... lds):
+// lane l's 16 bytes at byte offset `off` land at lds + 16 l.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rs, unsigned char* lds, uint32_t off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (QA_LDS void*)lds, 16, off, 0, 0, 0);
+}
+
 // s_waitcnt vmcnt(N) leaving expcnt / lgkmcnt unconstrained (gfx9 encoding).
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -521,40 +530,66 @@ __global__ void __launch_bounds__(64 * (WGM * WGN * KG + PW)) gemm_dma_kernel(co
     woff[j] = n >= 0 ? (uint32_t)(((int64_t)n * p.ldb + wkc[j]) * 2) : OOB;
   }
 
-  auto issue = [&](int kidx, int buf) {
+  // The DMA's LDS destination goes in M0, which must be wave-uniform: with
+  // the wave index in a scalar register it is scalar arithmetic, instead of a
+  // v_readfirstlane (and its hazard wait) per instruction.
+  const int dwave_s = wave_uniform(dwave);
+  // One ring stage's DMA, each chunk checked against the k range (rows past
+  // M / N carry OOB, which the buffer unit answers with zeros).
+  auto issue_checked = [&](int kidx, int buf) {
 #pragma unroll
     for (int pl = 0; pl < PL; ++pl) {
-    const int k0 = kbeg + kidx * SK + pl * BK;
-    unsigned char* sb = smem + buf * STAGE + pl * PLANE;
+      const int k0 = kbeg + kidx * SK + pl * BK;
+      unsigned char* sb = smem + buf * STAGE + pl * PLANE;
 #pragma unroll
-    for (int j = 0; j < AJ; ++j) {
-      uint32_t off;
-      if constexpr (CV) {
-        const int k = k0 + akc[j];
-        const int g = cg[j], ic = cic[j];  // tap g = 3 kh + kw
-        cic[j] += BK;  // the next plane: 64 channels on (c >= 64: at most one wrap)
-        if (cic[j] >= p.cv_c) {
-          cic[j] -= p.cv_c;
-          ++cg[j];
+      for (int j = 0; j < AJ; ++j) {
+        uint32_t off;
+        if constexpr (CV) {
+          const int k = k0 + akc[j];
+          const int g = cg[j], ic = cic[j];  // tap g = 3 kh + kw
+          cic[j] += BK;  // the next plane: 64 channels on (c >= 64: at most one wrap)
+          if (cic[j] >= p.cv_c) {
+            cic[j] -= p.cv_c;
+            ++cg[j];
+          }
+          const int kh = (g * 11) >> 5, kw = g - 3 * kh;   // g / 3 for g < 9
+          const int ih = cih[j] + kh, iw = ciw[j] + kw;
+          const bool ok =
+              k < kend && (unsigned)ih < (unsigned)p.cv_h && (unsigned)iw < (unsigned)p.cv_w;
+          off = ok ? (uint32_t)(((cpix[j] + ih * p.cv_w + iw) * p.cv_c + ic) * 2) : OOB;
+        } else {
+          const bool ok = k0 + akc[j] < kend && aoff[j] != OOB;
+          off = ok ? aoff[j] + (uint32_t)k0 * 2u : OOB;
         }
-        const int kh = (g * 11) >> 5, kw = g - 3 * kh;   // g / 3 for g < 9
-        const int ih = cih[j] + kh, iw = ciw[j] + kw;
-        const bool ok = k < kend && (unsigned)ih < (unsigned)p.cv_h && (unsigned)iw < (unsigned)p.cv_w;
-        off = ok ? (uint32_t)(((cpix[j] + ih * p.cv_w + iw) * p.cv_c + ic) * 2) : OOB;
-      } else {
-        const bool ok = k0 + akc[j] < kend && aoff[j] != OOB;
-        off = ok ? aoff[j] + (uint32_t)k0 * 2u : OOB;
+        dma16(rsa, sb + (j * NW + dwave_s) * 1024, off);
       }
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (QA_LDS void*)(sb + (j * NW + dwave) * 1024),
-                                               16, off, 0, 0, 0);
-    }
 #pragma unroll
-    for (int j = 0; j < BJ; ++j) {
-      const bool ok = k0 + wkc[j] < kend && woff[j] != OOB;
-      const uint32_t off = ok ? woff[j] + (uint32_t)k0 * 2u : OOB;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rsw, (QA_LDS void*)(sb + SA + (j * NW + dwave) * 1024), 16, off, 0, 0, 0);
+      for (int j = 0; j < BJ; ++j) {
+        const bool ok = k0 + wkc[j] < kend && woff[j] != OOB;
+        const uint32_t off = ok ? woff[j] + (uint32_t)k0 * 2u : OOB;
+        dma16(rsw, sb + SA + (j * NW + dwave_s) * 1024, off);
+      }
     }
+  };
+  // A stage inside the k range needs no per-chunk check: OOB (rows past
+  // M / N) plus 2 k0 still lies past every buffer's range, so each
+  // instruction is one add.  The last stage of a ragged k range, and the
+  // convolution's gathered A, take the checked form.
+  auto issue = [&](int kidx, int buf) {
+    if (!CV && kbeg + (kidx + 1) * SK <= kend) {
+#pragma unroll
+      for (int pl = 0; pl < PL; ++pl) {
+        const uint32_t k2 = (uint32_t)(kbeg + kidx * SK + pl * BK) * 2u;
+        unsigned char* sb = smem + buf * STAGE + pl * PLANE;
+#pragma unroll
+        for (int j = 0; j < AJ; ++j)
+          dma16(rsa, sb + (j * NW + dwave_s) * 1024, aoff[j] + k2);
+#pragma unroll
+        for (int j = 0; j < BJ; ++j)
+          dma16(rsw, sb + SA + (j * NW + dwave_s) * 1024, woff[j] + k2);
+      }
+    } else {
+      issue_checked(kidx, buf);
     }
   };
 
