@@ -457,6 +457,64 @@ def phase_stamps(pkg, host, ctx, warmup, steps):
                     "two layers of the last graph replay"}
 
 
+def phase_stamps_prefill(pkg, host, ctx, launches=3):
+    """The 300 s forward's large GEMM shapes (decoder prefill at 4352 rows,
+    the tower's fc1 at 3900) on the measurement build: eager back-to-back
+    launches of one shape, the per-block records of the last one, split by
+    the round of tiles each block ran in (one block per CU at a time, started
+    in dispatch order); per round, medians over its blocks (us from the
+    launch's first block start)."""
+    L = pkg.lib()
+    L.qa_phase_stamps_read.argtypes = [ctypes.c_void_p] * 4
+    slots, blocks, words = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    L.qa_phase_stamps_read(None, ctypes.byref(slots), ctypes.byref(blocks), ctypes.byref(words))
+    ncu = 256
+    cases = [("qkv", 4352, 4096, 1024, 0, False), ("o", 4352, 1024, 2048, pkg.ACCUMULATE, False),
+             ("gate|up", 4352, 6144, 1024, pkg.EPI_SILU_MUL, False),
+             ("down", 4352, 1024, 3072, pkg.ACCUMULATE, False),
+             ("tower fc1", 3900, 3584, 896, pkg.EPI_GELU, True)]
+    out = []
+    for name, m, n, k, flags, bias in cases:
+        a = host.synth_normal(0, 1, (m, k))
+        w = host.synth_normal(0, 2, (n, k), 0, 0.02)
+        nout = n // 2 if flags & pkg.EPI_SILU_MUL else n
+        da, dw = ctx.to_device(a), ctx.to_device(w)
+        dc = ctx.to_device(host.synth_normal(0, 4, (m, nout)))
+        db = ctx.to_device(host.synth_normal(0, 3, (n,), 0, 0.01)) if bias else None
+        desc = pkg.linear_desc(pkg.F16, m, n, k, da, dw, dc, flags=flags, bias=db, ldc=nout)
+        for _ in range(10):
+            ctx.linear(desc)
+        ctx.sync()
+        pkg.check(L.qa_phase_stamps_clear())
+        for _ in range(launches):
+            ctx.linear(desc)
+        ctx.sync()
+        rec = np.zeros((slots.value, blocks.value, words.value), np.uint64)
+        pkg.check(L.qa_phase_stamps_read(rec.ctypes.data, None, None, None))
+        for b in (da, dw, dc, db):
+            if b is not None:
+                b.free()
+        runs = [rec[s][rec[s][:, 0] > 0].astype(np.int64) for s in range(slots.value)]
+        r = sorted([x for x in runs if len(x)], key=lambda x: int(x[:, 0].min()))[-1]
+        t = [(r[:, i] - r[:, 0].min()) / 100.0 for i in range(5)]  # 100 MHz ticks -> us
+        # blocks start in dispatch order as CUs free up: the i-th block to
+        # start ran in round i // (one block per CU)
+        rnd = np.empty(len(r), int)
+        rnd[np.argsort(t[0], kind="stable")] = np.arange(len(r)) // ncu
+        rounds = []
+        for q in sorted(set(rnd.tolist())):
+            s = rnd == q
+            med = lambda x: round(float(np.median(x[s])), 2)  # noqa: E731
+            rounds.append({"blocks": int(s.sum()), "start": med(t[0]), "fill": med(t[1] - t[0]),
+                           "loop": med(t[2] - t[1]), "park": med(t[3] - t[2]),
+                           "stores": med(t[4] - t[3]), "last_end": round(float(t[4][s].max()), 2)})
+        out.append({"site": name, "m": m, "n": n, "k": k, "blocks": int(len(r)),
+                    "span": round(float(t[4].max()), 2), "rounds": rounds})
+    return {"phase_stamps_prefill": out,
+            "note": "measurement build (-DQA_PHASE_STAMPS), f16, eager launches; per round of "
+                    "tiles, medians over its blocks, us from the first block start"}
+
+
 def config2_pair_descs(pkg, host, ctx, warm):
     """Config 2's MLP block as launch pairs (gate|up + SiLU.up, then down +
     residual, M = 512): warm one weight set, cold 16 distinct sets (320 MB).
@@ -746,6 +804,10 @@ def main():
                     help="config 3 on the measurement build (make -C qwen3-aligner-wgpu_amd/csrc "
                          "stamps): per-block phase timestamps of the last two layers' GEMMs in a "
                          "graph replay, as a table of medians (one JSON line)")
+    ap.add_argument("--phase-stamps-prefill", action="store_true",
+                    help="the 300 s forward's prefill GEMM shapes and the tower's fc1 on the "
+                         "measurement build: per-block phase timestamps of one launch each, split "
+                         "by round of tiles (one JSON line)")
     ap.add_argument("--warm", action="store_true",
                     help="with --site: repeat layer 0's (or config 1's first) W instead of cycling")
     ap.add_argument("--vs-hipblaslt", action="store_true",
@@ -759,7 +821,7 @@ def main():
               "token rows with no exchange; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
-    if args.phase_stamps:
+    if args.phase_stamps or args.phase_stamps_prefill:
         os.environ["QA_BUILD"] = "stamps"  # before the package loads its libraries
     if args.vs_hipblaslt:
         # torch's own HIP runtime and BLAS libraries first: loaded after this
@@ -794,6 +856,11 @@ def main():
     if args.phase_stamps:
         with pkg.Context(0) as ctx:
             print(json.dumps(phase_stamps(pkg, host, ctx, args.warmup, args.steps)), flush=True)
+        return
+
+    if args.phase_stamps_prefill:
+        with pkg.Context(0) as ctx:
+            print(json.dumps(phase_stamps_prefill(pkg, host, ctx)), flush=True)
         return
 
     if args.e2e_only:
