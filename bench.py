@@ -349,8 +349,12 @@ def site_protocol(host, ctx, ss, warm_iters=200, cold_iters=280):
     for s, descs in ss.descs.items():
         cold = dist(host.time_linears_each(ss.ctx, descs, 20, cold_iters))
         warm = dist(host.time_linears_each(ss.ctx, descs[:1], 20, warm_iters))
-        out[s] = {"cold": cold, "warm": warm,
-                  "tflops_cold_median": round(ss.flops(s) / (cold["median"] * 1e-6) / 1e12, 1)}
+        cold_k = dist(host.time_linears_stamped(ss.ctx, descs, 20, cold_iters))
+        warm_k = dist(host.time_linears_stamped(ss.ctx, descs[:1], 20, warm_iters))
+        out[s] = {"cold": cold, "warm": warm, "cold_kernel": cold_k, "warm_kernel": warm_k,
+                  "tflops_cold_median": round(ss.flops(s) / (cold["median"] * 1e-6) / 1e12, 1),
+                  "tflops_cold_kernel_median":
+                      round(ss.flops(s) / (cold_k["median"] * 1e-6) / 1e12, 1)}
     seq = [ss.descs[s][li] for li in range(DEC["layers"]) for s in ss.sites]
     ms = host.time_linears_each(ss.ctx, seq, 20, 2 * len(seq))
     step_ms = float(ms.sum()) / 2
@@ -543,15 +547,24 @@ def config1_protocol(pkg, host, ctx):
     descs = [pkg.linear_desc(pkg.F16, m, n, k, a, w, c) for w in ws]
     warm = dist(host.time_linears_each(ctx, descs[:1], 20, 200))
     cold = dist(host.time_linears_each(ctx, descs, 20, 288))
+    warm_k = dist(host.time_linears_stamped(ctx, descs[:1], 20, 200))
+    cold_k = dist(host.time_linears_stamped(ctx, descs, 20, 288))
     algo = 2 * (m * k + n * k + m * n)
     for b in [a, c] + ws:
         b.free()
     f = 2 * m * n * k
-    return {"warm": warm, "cold": cold, "algorithmic_bytes": algo,
+    return {"warm": warm, "cold": cold, "warm_kernel": warm_k, "cold_kernel": cold_k,
+            "algorithmic_bytes": algo,
             "hbm_gbs_cold_median": round(algo / (cold["median"] * 1e-6) / 1e9, 1),
             "hbm_frac_cold_median": round(algo / (cold["median"] * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
+            "hbm_gbs_cold_kernel_median": round(algo / (cold_k["median"] * 1e-6) / 1e9, 1),
+            "hbm_frac_cold_kernel_median":
+                round(algo / (cold_k["median"] * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
             "tflops_cold_median": round(f / (cold["median"] * 1e-6) / 1e12, 1),
-            "tflops_warm_median": round(f / (warm["median"] * 1e-6) / 1e12, 1)}
+            "tflops_warm_median": round(f / (warm["median"] * 1e-6) / 1e12, 1),
+            "note": "cold / warm: event-to-event intervals of back-to-back launches (each with its "
+                    "share of the launch gap); *_kernel: the same launches timed by the kernel's "
+                    "own dispatch (qa_time_next_launch), kernel time alone"}
 
 
 def config2_protocol(pkg, host, ctx):
@@ -570,10 +583,14 @@ def config2_protocol(pkg, host, ctx):
                   pkg.linear_desc(pkg.F16, m, hid, it, act, dn, x, flags=pkg.ACCUMULATE)]
     warm = host.time_linears_each(ctx, descs[:2], 20, 400)
     cold = host.time_linears_each(ctx, descs, 20, 416)
+    warm_k = host.time_linears_stamped(ctx, descs[:2], 20, 400)
+    cold_k = host.time_linears_stamped(ctx, descs, 20, 416)
     pair = lambda ms: ms[0::2] + ms[1::2]  # noqa: E731
     f = 2 * m * 2 * it * hid + 2 * m * hid * it
     out = {"warm": dist(pair(warm)), "cold": dist(pair(cold)),
-           "gu_cold": dist(cold[0::2]), "down_cold": dist(cold[1::2])}
+           "gu_cold": dist(cold[0::2]), "down_cold": dist(cold[1::2]),
+           "warm_kernel": dist(pair(warm_k)), "cold_kernel": dist(pair(cold_k)),
+           "gu_cold_kernel": dist(cold_k[0::2]), "down_cold_kernel": dist(cold_k[1::2])}
     out["tflops_cold_median"] = round(f / (out["cold"]["median"] * 1e-6) / 1e12, 1)
     for b in [x, act] + [b for s in sets for b in s]:
         b.free()

@@ -182,8 +182,9 @@ int qa_prefetch_hint(qa_ctx* ctx, const void* ptr, size_t bytes);
  * qa_prefetch_hint) records the start and the end of its GEMM kernel into
  * these HIP events (hipEvent_t, created by the caller; either may be null),
  * stamped by the kernel's dispatch itself (hipExtLaunchKernel) rather than by
- * event packets queued between kernels, which add a gap of their own.  A
- * split-K reduce kernel after the GEMM is not inside the pair.  The launch
+ * event packets queued between kernels, which add a gap of their own.  With
+ * K split, the GEMM kernel stamps the start and the split-K reduce kernel
+ * after it the end, so the pair spans both.  The launch
  * that takes the events over clears them; under stream capture that launch
  * fails with QA_EINVAL (a captured dispatch does not stamp them on replay).
  * No counterpart in the reference; for per-kernel timing in harnesses

@@ -605,6 +605,28 @@ int qah_time_linears_each(qa_ctx* ctx, const qa_linear_desc* descs, int ndesc, i
   return rc;
 }
 
+int qah_time_linears_stamped(qa_ctx* ctx, const qa_linear_desc* descs, int ndesc, int warmup,
+                             int iters, float* ms_each) {
+  if (!ctx || !descs || ndesc <= 0 || warmup < 0 || iters <= 0 || !ms_each) return QA_EINVAL;
+  for (int i = 0; i < warmup; ++i)
+    if (int rc = qa_linear(ctx, &descs[i % ndesc])) return rc;
+  std::vector<hipEvent_t> ev(2 * (size_t)iters, nullptr);
+  int rc = QA_OK;
+  for (auto& e : ev)
+    if (rc == QA_OK && hipEventCreate(&e) != hipSuccess) rc = QA_EDEVICE;
+  if (rc == QA_OK) rc = qa_sync(ctx);
+  for (int i = 0; i < iters && rc == QA_OK; ++i) {
+    rc = qa_time_next_launch(ctx, ev[2 * (size_t)i], ev[2 * (size_t)i + 1]);
+    if (rc == QA_OK) rc = qa_linear(ctx, &descs[i % ndesc]);
+  }
+  if (int rs = qa_sync(ctx); rc == QA_OK) rc = rs;
+  for (int i = 0; i < iters && rc == QA_OK; ++i)
+    rc = hip_status(hipEventElapsedTime(&ms_each[i], ev[2 * (size_t)i], ev[2 * (size_t)i + 1]));
+  for (auto& e : ev)
+    if (e) (void)hipEventDestroy(e);
+  return rc;
+}
+
 int qah_copy_calibration(qa_ctx* ctx, size_t bytes, int reps) {
   if (!ctx || bytes % 16 || reps <= 0) return QA_EINVAL;
   Buffer a, b;

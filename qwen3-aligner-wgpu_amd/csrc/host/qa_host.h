@@ -288,6 +288,13 @@ int qah_time_linear(qa_ctx* ctx, const qa_linear_desc* desc, int warmup, int ite
 int qah_time_linears_each(qa_ctx* ctx, const qa_linear_desc* descs, int ndesc, int warmup,
                           int iters, float* ms_each);
 
+/* The same launches, each timed by its own kernels' dispatches
+ * (qa_time_next_launch): ms_each[i] is launch i's kernel time alone, from
+ * the GEMM's start to its end (to the split-K reduce's end when K is split),
+ * without the gap between launches. */
+int qah_time_linears_stamped(qa_ctx* ctx, const qa_linear_desc* descs, int ndesc, int warmup,
+                             int iters, float* ms_each);
+
 /* A plain 16-byte-per-thread copy of `bytes` between two fresh buffers,
  * `reps` times: the known-size reference that calibrates the FETCH_SIZE /
  * WRITE_SIZE counters. */

@@ -1050,17 +1050,18 @@ hipError_t launch_reg(const Plan& plan, const GemmParams& p, int batch, hipStrea
 }
 
 template <int DT, int EPI>
-hipError_t launch_reduce(const GemmParams& p, hipStream_t s) {
+hipError_t launch_reduce(const GemmParams& p, hipStream_t s, const Stamps& ts) {
   const int nout = EPI == EPI_SILU ? p.N / 2 : p.N;
   const int64_t threads = (int64_t)p.M * (nout / 4);
-  hipLaunchKernelGGL((splitk_reduce_kernel<DT, EPI>), dim3((unsigned)((threads + 255) / 256)),
-                     dim3(256), 0, s, p);
-  return hipGetLastError();
+  return launch_kernel(splitk_reduce_kernel<DT, EPI>, dim3((unsigned)((threads + 255) / 256)),
+                       dim3(256), s, ts, p);
 }
 
 template <int DT, int EPI>
 hipError_t launch_epi(const Plan& plan, const GemmParams& p, int batch, hipStream_t s,
-                      const Stamps& ts) {
+                      const Stamps& ts_in) {
+  // split K: the GEMM's dispatch stamps the start, the reduce's the end
+  const Stamps ts = plan.splits > 1 ? Stamps{ts_in.t0, nullptr} : ts_in;
   hipError_t e;
   if (plan.conv) {  // implicit-GEMM convolution (qa_conv2d_3x3s2)
     if constexpr (EPI == EPI_SILU) return hipErrorInvalidValue;  // never planned
@@ -1108,7 +1109,7 @@ hipError_t launch_epi(const Plan& plan, const GemmParams& p, int batch, hipStrea
     }
   }
   if (e != hipSuccess || plan.splits == 1) return e;
-  return launch_reduce<DT, EPI>(p, s);
+  return launch_reduce<DT, EPI>(p, s, Stamps{nullptr, ts_in.t1});
 }
 
 template <int DT>

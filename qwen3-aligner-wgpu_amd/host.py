@@ -90,6 +90,7 @@ def declare(L: ctypes.CDLL) -> None:
     L.qah_time_linear.argtypes = [_vp, _vp, _i, _i, _dp]
     L.qah_copy_calibration.argtypes = [_vp, _sz, _i]
     L.qah_time_linears_each.argtypes = [_vp, _vp, _i, _i, _i, _vp]
+    L.qah_time_linears_stamped.argtypes = [_vp, _vp, _i, _i, _i, _vp]
     for name in ("qah_decoder_create", "qah_decoder_load_layer", "qah_decoder_set_inputs",
                  "qah_decoder_prefill_linears", "qah_decoder_read", "qah_decoder_time",
                  "qah_decoder_profile_sites", "qah_encoder_create", "qah_encoder_load_layer",
@@ -622,6 +623,16 @@ def time_linears_each(ctx, descs, warmup: int, iters: int) -> np.ndarray:
     out = np.zeros(iters, np.float32)
     check(host_lib().qah_time_linears_each(ctx.handle, arr, len(descs), warmup, iters,
                                            out.ctypes.data))
+    return out
+
+
+def time_linears_stamped(ctx, descs, warmup: int, iters: int) -> np.ndarray:
+    """qah_time_linears_stamped: per-launch kernel ms (dispatch-stamped events,
+    no inter-launch gap) of `iters` back-to-back launches cycling through `descs`."""
+    arr = (type(descs[0]) * len(descs))(*descs)
+    out = np.zeros(iters, np.float32)
+    check(host_lib().qah_time_linears_stamped(ctx.handle, arr, len(descs), warmup, iters,
+                                              out.ctypes.data))
     return out
 
 

@@ -363,3 +363,72 @@ def test_time_next_launch_stamps_the_kernel(ctx, pkg, orc):
             hip.hipEventDestroy(e)
     assert np.array_equal(stamped, plain)
     assert np.array_equal(again, plain)
+
+
+def test_time_next_launch_spans_the_split_k_reduce(ctx, pkg, orc):
+    """With K split, the GEMM kernel's dispatch stamps the start event and the
+    split-K reduce kernel's the stop event: a positive interval, and the
+    result (GEMM + reduce + residual) within 1 ulp of the exactly rounded one."""
+    import ctypes
+
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+    hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p,
+                                        ctypes.c_void_p]
+    hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+    ev = [ctypes.c_void_p(), ctypes.c_void_p()]
+    for e in ev:
+        assert hip.hipEventCreate(ctypes.byref(e)) == 0
+    rng = np.random.default_rng(13)
+    m, n, k = 512, 1024, 3072
+    a = _h16(orc, rng.standard_normal((m, k)), 0)
+    w = _h16(orc, 0.02 * rng.standard_normal((n, k)), 0)
+    c0 = _h16(orc, rng.standard_normal((m, n)), 0)
+    da, dw, dc = ctx.to_device(a), ctx.to_device(w), ctx.to_device(c0)
+    desc = pkg.linear_desc(0, m, n, k, da, dw, dc, flags=pkg.ACCUMULATE)
+    os.environ["QA_SPLITS"] = "2"
+    try:
+        pkg.check(pkg.lib().qa_time_next_launch(ctx.handle, ev[0], ev[1]))
+        ctx.linear(desc)
+        ctx.sync()
+        ms = ctypes.c_float()
+        assert hip.hipEventElapsedTime(ctypes.byref(ms), ev[0], ev[1]) == 0
+        assert ms.value > 0.0, ms.value
+        got = ctx.download(dc, c0.shape)
+    finally:
+        del os.environ["QA_SPLITS"]
+        for b in (da, dw, dc):
+            b.free()
+        for e in ev:
+            hip.hipEventDestroy(e)
+    exact = orc.linear(0, a, w, c0.copy(), flags=orc.ACCUMULATE | orc.EXACT)
+    assert_parity(got, exact, orc, 0, ulp_tol=1)
+
+
+def test_stamped_per_launch_timer(ctx, pkg, orc):
+    """qah_time_linears_stamped (the benchmark's kernel-only per-launch
+    figures): positive per launch, and each launch's kernel time is at most
+    the event-to-event interval of the same back-to-back launches (which adds
+    the gap between them), compared on medians; unsplit and split-K."""
+    from qwen3_aligner_wgpu_amd import host
+
+    rng = np.random.default_rng(14)
+    m, n, k = 512, 1024, 3072
+    a = _h16(orc, rng.standard_normal((m, k)), 0)
+    w = _h16(orc, 0.02 * rng.standard_normal((n, k)), 0)
+    da, dw, dc = ctx.to_device(a), ctx.to_device(w), ctx.alloc(m * n * 2)
+    desc = pkg.linear_desc(0, m, n, k, da, dw, dc)
+    try:
+        for splits in ("1", "2"):
+            os.environ["QA_SPLITS"] = splits
+            try:
+                kern = host.time_linears_stamped(ctx, [desc], 5, 40)
+                each = host.time_linears_each(ctx, [desc], 5, 40)
+            finally:
+                del os.environ["QA_SPLITS"]
+            assert (kern > 0).all(), kern
+            assert np.median(kern) <= np.median(each) * 1.05, (splits, np.median(kern),
+                                                               np.median(each))
+    finally:
+        for b in (da, dw, dc):
+            b.free()
