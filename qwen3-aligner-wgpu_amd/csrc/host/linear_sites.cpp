@@ -17,6 +17,7 @@
 #include <thread>
 
 #include "../half_bits.h"
+#include "../qa_internal.h"
 #include "qa_host.h"
 #include "timing.hpp"
 
@@ -392,6 +393,55 @@ __global__ void copy_kernel(const uint4* __restrict__ src, uint4* __restrict__ d
     dst[i] = src[i];
 }
 
+__device__ uint64_t mix64(uint64_t z) {  // SplitMix64's finaliser
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+  return z ^ (z >> 31);
+}
+
+// Input i of the SiLU.up check: special values for the first 4096, then
+// random f32 bit patterns (every third) and values in [-16, 16) x {1, 0.01}.
+__device__ void silu_check_input(uint64_t seed, int64_t i, float* g, float* u) {
+  const float sp[20] = {0.0f, -0.0f, 1e-8f, -1e-8f, 6e-8f, -6e-8f, 1e-5f, -1e-5f, 65504.f,
+                        -65504.f, 70000.f, -70000.f, 1e30f, -1e30f, 88.f, -88.f, 20.f, -20.f,
+                        0.5f, -0.5f};
+  const uint64_t r = mix64(seed + 0x9e3779b97f4a7c15ull * (uint64_t)(i + 1));
+  if (i < 4096) {
+    *g = sp[i % 20];
+    *u = sp[(i / 20) % 20];
+  } else if (i % 3 == 0) {
+    *g = __uint_as_float((uint32_t)r);
+    *u = __uint_as_float((uint32_t)(r >> 32));
+  } else {
+    const float sg = (i % 7) ? 1.0f : 0.01f;
+    *g = ((float)(r & 0xffffff) / 8388608.0f - 1.0f) * 16.0f * sg;
+    *u = ((float)((r >> 24) & 0xffffff) / 8388608.0f - 1.0f) * 8.0f;
+  }
+}
+
+// silu_mul_f16x2 against silu_mul in f32 followed by a separate f16 rounding
+// (the empty asm keeps the compiler from fusing the two): outputs that differ,
+// other than two NaNs, are counted.
+__global__ void silu_check_kernel(uint64_t seed, int64_t pairs, unsigned long long* bad) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= pairs) return;
+  float g[2], u[2];
+  silu_check_input(seed, 2 * i, &g[0], &u[0]);
+  silu_check_input(seed, 2 * i + 1, &g[1], &u[1]);
+  const uint32_t got = qa::silu_mul_f16x2(g[0], g[1], u[0], u[1]);
+  unsigned n = 0;
+  for (int e = 0; e < 2; ++e) {
+    float v = qa::silu_mul((float)(_Float16)g[e], (float)(_Float16)u[e]);
+    asm volatile("" : "+v"(v));
+    const uint32_t want = __builtin_bit_cast(uint16_t, (_Float16)v);
+    const uint32_t have = (got >> (16 * e)) & 0xffffu;
+    const bool nans = (want & 0x7c00u) == 0x7c00u && (want & 0x3ffu) &&
+                      (have & 0x7c00u) == 0x7c00u && (have & 0x3ffu);
+    n += want != have && !nans;
+  }
+  if (n) atomicAdd(bad, (unsigned long long)n);
+}
+
 }  // namespace
 
 extern "C" {
@@ -624,6 +674,25 @@ int qah_time_linears_stamped(qa_ctx* ctx, const qa_linear_desc* descs, int ndesc
     rc = hip_status(hipEventElapsedTime(&ms_each[i], ev[2 * (size_t)i], ev[2 * (size_t)i + 1]));
   for (auto& e : ev)
     if (e) (void)hipEventDestroy(e);
+  return rc;
+}
+
+int qah_check_silu_f16x2(qa_ctx* ctx, int64_t pairs, uint64_t seed, int64_t* mismatches) {
+  if (!ctx || pairs <= 0 || pairs > ((int64_t)1 << 31) || !mismatches) return QA_EINVAL;
+  Buffer cnt;
+  int rc = alloc(ctx, sizeof(unsigned long long), &cnt);
+  hipStream_t s = (hipStream_t)qa_ctx_stream(ctx);
+  unsigned long long host = 0;
+  if (rc == QA_OK) rc = qa_upload(ctx, cnt.ptr, 0, &host, sizeof host);
+  if (rc == QA_OK) {
+    hipLaunchKernelGGL(silu_check_kernel, dim3((unsigned)((pairs + 255) / 256)), dim3(256), 0, s,
+                       seed, pairs, (unsigned long long*)cnt.ptr);
+    rc = hip_status(hipGetLastError());
+  }
+  if (rc == QA_OK) rc = qa_sync(ctx);
+  if (rc == QA_OK) rc = qa_download(ctx, &host, cnt.ptr, 0, sizeof host);
+  release(ctx, &cnt);
+  if (rc == QA_OK) *mismatches = (int64_t)host;
   return rc;
 }
 

@@ -288,6 +288,13 @@ int qah_time_linear(qa_ctx* ctx, const qa_linear_desc* desc, int warmup, int ite
 int qah_time_linears_each(qa_ctx* ctx, const qa_linear_desc* descs, int ndesc, int warmup,
                           int iters, float* ms_each);
 
+/* Checks the f16 SiLU.up epilogue's packed arithmetic (silu_mul_f16x2 in
+ * qa_internal.h) on the device against silu_mul in f32 followed by a separate
+ * round-to-nearest-even to f16, on 2 * pairs inputs generated from `seed`
+ * (special values, random f32 bit patterns, values in [-16, 16)):
+ * *mismatches = outputs that differ (two NaNs count as equal). */
+int qah_check_silu_f16x2(qa_ctx* ctx, int64_t pairs, uint64_t seed, int64_t* mismatches);
+
 /* The same launches, each timed by its own kernels' dispatches
  * (qa_time_next_launch): ms_each[i] is launch i's kernel time alone, from
  * the GEMM's start to its end (to the split-K reduce's end when K is split),

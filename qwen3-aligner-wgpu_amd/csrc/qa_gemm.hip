@@ -183,49 +183,7 @@ __device__ __forceinline__ void exec_barrier() {
 // IEEE divide cost ~30-40 VALU instructions per output, which made the
 // SiLU.up epilogue a quarter of the gate|up kernel.  Either error is a few f32
 // ulps, far below the 16-bit rounding that follows.
-constexpr float kLog2e = 1.44269504088896341f;
-
-// The erf GELU is gelu_erf (qa_internal.h).
-//
-// g * sigmoid(g) * u with sigmoid(g) = 1 / (1 + 2^(-g log2 e)), the reference
-// GPU kernel's form (src/shaders.rs:1411-1450).
-__device__ __forceinline__ float silu_mul(float g, float u) {
-  return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g * kLog2e)) * u;
-}
-
-// Two f16 SiLU.up outputs packed in one word: the arithmetic of silu_mul on
-// the f16-rounded g and u and the f16 rounding of the result, bit for bit
-// (16.7 M random and special inputs against the general path below), in 7
-// VALU instructions per output instead of 11.  g and u are rounded in pairs
-// (v_cvt_pk_f16_f32) and read straight as f16 operands of v_fma_mix (no
-// widening), and each output is rounded into its half of the word by
-// v_fma_mixlo / v_fma_mixhi.  -g log2 e and g r are the same single f32
-// roundings of the same products as the multiplies they replace; the addend
-// neg(0) keeps a -0 gate's sign through g r.  The first s_nop is the wait
-// state gfx950 needs before a VALU instruction reads the result of a
-// transcendental (v_rcp_f32): the compiler inserts it ahead of its own
-// instructions but not ahead of an asm statement, which without it read the
-// register's previous value (1 + 2^t).  The second covers the partial
-// (half-word) write of v_fma_mixlo read back by v_fma_mixhi.
-__device__ __forceinline__ uint32_t silu_mul_f16x2(float g0, float g1, float u0, float u1) {
-  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-  const uint32_t gw = __builtin_bit_cast(uint32_t, h2{(_Float16)g0, (_Float16)g1});
-  const uint32_t uw = __builtin_bit_cast(uint32_t, h2{(_Float16)u0, (_Float16)u1});
-  const float c = -kLog2e;
-  float t0, t1, s0, s1;
-  uint32_t o;
-  asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[1,0,0]" : "=v"(t0) : "v"(gw), "v"(c));
-  asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(t1) : "v"(gw), "v"(c));
-  const float r0 = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(t0));
-  const float r1 = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(t1));
-  asm("s_nop 0\n\tv_fma_mix_f32 %0, %1, %2, neg(0) op_sel_hi:[1,0,0]" : "=v"(s0) : "v"(gw), "v"(r0));
-  asm("s_nop 0\n\tv_fma_mix_f32 %0, %1, %2, neg(0) op_sel:[1,0,0] op_sel_hi:[1,0,0]"
-      : "=v"(s1) : "v"(gw), "v"(r1));
-  asm("v_fma_mixlo_f16 %0, %1, %2, 0 op_sel_hi:[0,1,0]" : "=v"(o) : "v"(s0), "v"(uw));
-  asm("s_nop 0\n\tv_fma_mixhi_f16 %0, %1, %2, 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]"
-      : "+v"(o) : "v"(s1), "v"(uw));
-  return o;
-}
+// The erf GELU is gelu_erf, SiLU.up silu_mul / silu_mul_f16x2 (qa_internal.h).
 
 // Output stores carry sc1 (device scope): the lines are written through the
 // XCD's L2 as they are stored, so the end-of-kernel release has no dirty

@@ -71,7 +71,6 @@ __device__ __forceinline__ int fastdiv(int n, FastDiv f) {
   return (int)(((uint64_t)(uint32_t)n * f.m) >> f.p);
 }
 
-// Kernel parameters (passed by value).  Element units throughout.
 // erf-form GELU, 0.5 x (1 + erf(x / sqrt 2)), with erf from Abramowitz &
 // Stegun 7.1.26 (|error| <= 1.5e-7) on v_exp_f32 / v_rcp_f32: the form of the
 // reference's `audio_bias_gelu` (src/shaders.rs:2593-2625); the CPU twin calls
@@ -96,6 +95,46 @@ __device__ __forceinline__ float gelu_erf(float x) {
   return fmaf(-ax, p * t * e, fmaxf(x, -0.0f));
 }
 
+// g sigmoid(g) u with sigmoid(g) = 1 / (1 + 2^(-g log2 e)), in f32 on the
+// 16-bit g and u: the reference GPU kernel's form (src/shaders.rs:1411-1450).
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  constexpr float log2e = 1.44269504088896341f;
+  return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g * log2e)) * u;
+}
+
+// Two f16 SiLU.up outputs packed in one word: silu_mul on the f16-rounded g
+// and u, then one round-to-nearest-even to f16 of each f32 result, bit for
+// bit (qah_check_silu_f16x2 compares it with that reference on 16.7 M random
+// and special inputs), in 7.5 VALU instructions per output instead of 11.
+// g and u are rounded in pairs (v_cvt_pk_f16_f32) and read straight as f16
+// operands of v_fma_mix (no widening); each v_fma_mix_f32 rounds its product
+// once to f32, as the multiply it replaces, and the addend neg(0) keeps the
+// sign of a -0 product.  (v_fma_mixlo / mixhi_f16 would save the final
+// conversion but round the exact product straight to f16: 1 ulp off the
+// f32-then-f16 result in about 1 of 28000 outputs.)  The s_nop is the wait
+// state gfx950 needs before a VALU instruction reads the result of a
+// transcendental (v_rcp_f32): the compiler inserts it ahead of its own
+// instructions but not ahead of an asm statement, which without it read the
+// register's previous value (1 + 2^t).
+__device__ __forceinline__ uint32_t silu_mul_f16x2(float g0, float g1, float u0, float u1) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const uint32_t gw = __builtin_bit_cast(uint32_t, h2{(_Float16)g0, (_Float16)g1});
+  const uint32_t uw = __builtin_bit_cast(uint32_t, h2{(_Float16)u0, (_Float16)u1});
+  const float c = -1.44269504088896341f;
+  float t0, t1, s0, s1, p0, p1;
+  asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[1,0,0]" : "=v"(t0) : "v"(gw), "v"(c));
+  asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(t1) : "v"(gw), "v"(c));
+  const float r0 = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(t0));
+  const float r1 = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(t1));
+  asm("s_nop 0\n\tv_fma_mix_f32 %0, %1, %2, neg(0) op_sel_hi:[1,0,0]" : "=v"(s0) : "v"(gw), "v"(r0));
+  asm("s_nop 0\n\tv_fma_mix_f32 %0, %1, %2, neg(0) op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+      : "=v"(s1) : "v"(gw), "v"(r1));
+  asm("v_fma_mix_f32 %0, %1, %2, neg(0) op_sel_hi:[0,1,0]" : "=v"(p0) : "v"(s0), "v"(uw));
+  asm("v_fma_mix_f32 %0, %1, %2, neg(0) op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "=v"(p1) : "v"(s1), "v"(uw));
+  return __builtin_bit_cast(uint32_t, h2{(_Float16)p0, (_Float16)p1});
+}
+
+// Kernel parameters (passed by value).  Element units throughout.
 struct GemmParams {
   const uint16_t* a;
   const uint16_t* w;

@@ -91,6 +91,7 @@ def declare(L: ctypes.CDLL) -> None:
     L.qah_copy_calibration.argtypes = [_vp, _sz, _i]
     L.qah_time_linears_each.argtypes = [_vp, _vp, _i, _i, _i, _vp]
     L.qah_time_linears_stamped.argtypes = [_vp, _vp, _i, _i, _i, _vp]
+    L.qah_check_silu_f16x2.argtypes = [_vp, ctypes.c_int64, ctypes.c_uint64, _vp]
     for name in ("qah_decoder_create", "qah_decoder_load_layer", "qah_decoder_set_inputs",
                  "qah_decoder_prefill_linears", "qah_decoder_read", "qah_decoder_time",
                  "qah_decoder_profile_sites", "qah_encoder_create", "qah_encoder_load_layer",
@@ -634,6 +635,15 @@ def time_linears_stamped(ctx, descs, warmup: int, iters: int) -> np.ndarray:
     check(host_lib().qah_time_linears_stamped(ctx.handle, arr, len(descs), warmup, iters,
                                               out.ctypes.data))
     return out
+
+
+def check_silu_f16x2(ctx, pairs: int, seed: int = 1) -> int:
+    """qah_check_silu_f16x2: outputs of the f16 SiLU.up epilogue's packed
+    arithmetic that differ from silu_mul in f32 plus a separate f16 rounding,
+    over 2 * pairs generated inputs."""
+    bad = ctypes.c_int64()
+    check(host_lib().qah_check_silu_f16x2(ctx.handle, pairs, seed, ctypes.byref(bad)))
+    return bad.value
 
 
 def copy_calibration(ctx, nbytes: int, reps: int = 3) -> None:

@@ -432,3 +432,15 @@ def test_stamped_per_launch_timer(ctx, pkg, orc):
     finally:
         for b in (da, dw, dc):
             b.free()
+
+
+@pytest.mark.parametrize("seed", [1, 2])
+def test_silu_f16_packed_arithmetic_is_f32_then_f16(ctx, pkg, seed):
+    """The f16 SiLU.up epilogue's packed arithmetic (v_fma_mix on f16 operands,
+    paired conversions) gives, bit for bit, silu_mul in f32 followed by one
+    round-to-nearest-even to f16 (the reference shader's order, src/shaders.rs:
+    1411-1450), on 16.7 M inputs per seed: special values (+-0, subnormals, f16
+    overflow), random f32 bit patterns and ordinary values."""
+    from qwen3_aligner_wgpu_amd import host
+
+    assert host.check_silu_f16x2(ctx, 1 << 23, seed) == 0
