@@ -217,6 +217,14 @@ __device__ __forceinline__ void widen4(u32x2 w, float* v) {
   v[3] = Fmt<DT>::widen(w.y >> 16);
 }
 
+// v[e] += the f16 value e of the 4 packed in w (add_f16_half: no widening).
+__device__ __forceinline__ void add4_f16(u32x2 w, float* v) {
+  v[0] = add_f16_half<false>(w.x, v[0]);
+  v[1] = add_f16_half<true>(w.x, v[1]);
+  v[2] = add_f16_half<false>(w.y, v[2]);
+  v[3] = add_f16_half<true>(w.y, v[3]);
+}
+
 // Final values of 4 consecutive output columns [n, n+4) of row m -> C.
 // For SiLU, v holds the gate sums and u the up sums.  pre_old, when given,
 // holds the group's residual words, loaded earlier; otherwise they are read
@@ -254,6 +262,9 @@ __device__ __forceinline__ void epilogue4(const GemmParams& p, uint16_t* C, int 
         const float b = Fmt<DT>::widen(p.bias[m]);
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] += b;
+      } else if constexpr (DT == QA_F16) {
+        const u32x2 bw = pre_bias ? *pre_bias : *reinterpret_cast<const u32x2*>(p.bias + n);
+        add4_f16(bw, v);
       } else {
         float b[4];
         widen4<DT>(pre_bias ? *pre_bias : *reinterpret_cast<const u32x2*>(p.bias + n), b);
@@ -266,10 +277,14 @@ __device__ __forceinline__ void epilogue4(const GemmParams& p, uint16_t* C, int 
       for (int e = 0; e < 4; ++e) v[e] = gelu_erf(v[e]);
     }
     if (p.accumulate) {
-      float old[4];
-      widen4<DT>(pre_old ? *pre_old : *reinterpret_cast<const u32x2*>(dst), old);
+      if constexpr (DT == QA_F16) {
+        add4_f16(pre_old ? *pre_old : *reinterpret_cast<const u32x2*>(dst), v);
+      } else {
+        float old[4];
+        widen4<DT>(pre_old ? *pre_old : *reinterpret_cast<const u32x2*>(dst), old);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] += old[e];
+        for (int e = 0; e < 4; ++e) v[e] += old[e];
+      }
     }
   }
   store4<DT>(dst, v);

@@ -92,7 +92,26 @@ __device__ __forceinline__ float gelu_erf(float x) {
   const float e = __builtin_amdgcn_exp2f(x * x * (-0.5f * 1.44269504088896341f));  // e^{-a^2}
   const float p = (((h * 1.061405429f * t - h * 1.453152027f) * t + h * 1.421413741f) * t -
                    h * 0.284496736f) * t + h * 0.254829592f;
-  return fmaf(-ax, p * t * e, fmaxf(x, -0.0f));
+  // max(x, -0) as one v_max_f32: fmaxf adds a canonicalising v_max first,
+  // which only matters for a NaN x, and a NaN x makes the FMA NaN anyway
+  float mx;
+  asm("v_max_f32_e64 %0, %1, neg(0)" : "=v"(mx) : "v"(x));
+  return fmaf(-ax, p * t * e, mx);
+}
+
+// x + the f16 value in the low (hi = false) or high half of w, in f32 with
+// one rounding (the sum an f32 add of the widened value gives): v_fma_mix_f32
+// reads the half as an f16 operand, without a widening instruction.  x must
+// not come straight from a transcendental (an asm statement gets no wait
+// state ahead of it).
+template <bool HI>
+__device__ __forceinline__ float add_f16_half(uint32_t w, float x) {
+  float r;
+  if constexpr (HI)
+    asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(w), "v"(x));
+  else
+    asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(w), "v"(x));
+  return r;
 }
 
 // g sigmoid(g) u with sigmoid(g) = 1 / (1 + 2^(-g log2 e)), in f32 on the
