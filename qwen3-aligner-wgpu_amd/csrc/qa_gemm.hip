@@ -233,7 +233,10 @@ __device__ __forceinline__ void add4_f16(u32x2 w, float* v) {
 // VMEM operation before each store, the previous groups' stores included,
 // since vmcnt counts stores too; the qkv store phase measured 2.0 against
 // 1.16 us that way.)
-template <int DT, int EPI>
+// ACC: v_in comes straight from MFMA accumulators (the register-staged
+// kernel), which the v_fma_mix forms of the f16 adds must not read (see
+// add_f16_half); those launches take the widening adds.
+template <int DT, int EPI, bool ACC = false>
 __device__ __forceinline__ void epilogue4(const GemmParams& p, uint16_t* C, int m, int n,
                                           const float* v_in, const float* u_in,
                                           const u32x2* pre_old = nullptr,
@@ -262,7 +265,7 @@ __device__ __forceinline__ void epilogue4(const GemmParams& p, uint16_t* C, int 
         const float b = Fmt<DT>::widen(p.bias[m]);
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] += b;
-      } else if constexpr (DT == QA_F16) {
+      } else if constexpr (DT == QA_F16 && !ACC) {
         const u32x2 bw = pre_bias ? *pre_bias : *reinterpret_cast<const u32x2*>(p.bias + n);
         add4_f16(bw, v);
       } else {
@@ -277,7 +280,7 @@ __device__ __forceinline__ void epilogue4(const GemmParams& p, uint16_t* C, int 
       for (int e = 0; e < 4; ++e) v[e] = gelu_erf(v[e]);
     }
     if (p.accumulate) {
-      if constexpr (DT == QA_F16) {
+      if constexpr (DT == QA_F16 && !ACC) {
         add4_f16(pre_old ? *pre_old : *reinterpret_cast<const u32x2*>(dst), v);
       } else {
         float old[4];
@@ -348,7 +351,7 @@ __device__ __forceinline__ void finish_tile(const GemmParams& p, f32x16 (&acc)[F
         if (n >= p.N) continue;
         const float v[4] = {acc[fm][fn][4 * g], acc[fm][fn][4 * g + 1], acc[fm][fn][4 * g + 2],
                             acc[fm][fn][4 * g + 3]};
-        epilogue4<DT, EPI>(p, C, m, n, v, nullptr);
+        epilogue4<DT, EPI, true>(p, C, m, n, v, nullptr);
       }
     }
   }

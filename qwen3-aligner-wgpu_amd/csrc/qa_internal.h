@@ -93,17 +93,22 @@ __device__ __forceinline__ float gelu_erf(float x) {
   const float p = (((h * 1.061405429f * t - h * 1.453152027f) * t + h * 1.421413741f) * t -
                    h * 0.284496736f) * t + h * 0.254829592f;
   // max(x, -0) as one v_max_f32: fmaxf adds a canonicalising v_max first,
-  // which only matters for a NaN x, and a NaN x makes the FMA NaN anyway
+  // which only matters for a NaN x, and a NaN x makes the FMA NaN anyway.
+  // The instruction does not read %2 (e): that operand only orders the
+  // statement after x * x, a compiler instruction reading x, ahead of which
+  // the compiler puts any wait state x's producer needs (an MFMA's result,
+  // in the register-staged GEMM); it puts none ahead of an asm statement.
   float mx;
-  asm("v_max_f32_e64 %0, %1, neg(0)" : "=v"(mx) : "v"(x));
+  asm("v_max_f32_e64 %0, %1, neg(0)" : "=v"(mx) : "v"(x), "v"(e));
   return fmaf(-ax, p * t * e, mx);
 }
 
 // x + the f16 value in the low (hi = false) or high half of w, in f32 with
 // one rounding (the sum an f32 add of the widened value gives): v_fma_mix_f32
 // reads the half as an f16 operand, without a widening instruction.  x must
-// not come straight from a transcendental (an asm statement gets no wait
-// state ahead of it).
+// not come straight from a transcendental or an MFMA (an asm statement gets
+// no wait state ahead of it): the callers pass values read from LDS or
+// memory, or produced by ordinary VALU instructions.
 template <bool HI>
 __device__ __forceinline__ float add_f16_half(uint32_t w, float x) {
   float r;
