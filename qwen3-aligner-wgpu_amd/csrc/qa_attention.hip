@@ -98,7 +98,11 @@ struct AFmt<QA_F16> {
   // two 16-bit values.  Each difference is exact in f32 (a and h agree in
   // their leading bits), so v_fma_mix_f32 (-h) * 1 + a, which reads h
   // straight from its half of the packed word, gives the same bits as
-  // widening h and subtracting, in one instruction instead of two.
+  // widening h and subtracting, in one instruction instead of two.  a and b
+  // are v_exp_f32 results, and the compiler puts no wait state ahead of an
+  // asm statement; h = pack2(a, b) is a compiler instruction that reads both
+  // and precedes these by its data dependency, so the transcendental's
+  // one-instruction wait state has passed when they read a and b.
   __device__ static __forceinline__ uint32_t residue2(uint32_t h, float a, float b) {
     float d0, d1;
     asm("v_fma_mix_f32 %0, -%1, 1.0, %2 op_sel_hi:[1,0,0]" : "=v"(d0) : "v"(h), "v"(a));
