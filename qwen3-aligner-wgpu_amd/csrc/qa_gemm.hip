@@ -786,8 +786,58 @@ __global__ void __launch_bounds__(64 * (WGM * WGN * KG + PW)) gemm_dma_kernel(co
 #ifdef QA_PHASE_STAMPS
   st[2] = __builtin_amdgcn_s_memrealtime();
 #endif
+  // f16 SiLU.up, unsplit, one k group: the epilogue rounds g and u to f16
+  // before anything else, so the MMA waves park them rounded, as an f16
+  // [BM][BN + 4] tile: half the LDS bytes of the f32 tile, in one pass where
+  // the f32 tile of a 256-row tile needs two, and the store loop reads packed
+  // pairs straight into silu_mul_h2 (no conversions).  Same bits as the f32
+  // path below, which split launches (f32 partials) still take.
+  bool parked16 = false;
+  if constexpr (EPI == EPI_SILU && DT == QA_F16 && KG == 1) {
+    if (p.splits == 1) {
+      parked16 = true;
+      constexpr int LDH = BN + 4;  // halves per parked row
+      static_assert(BM * LDH * 2 <= SMEM, "f16 park fits the LDS");
+      uint16_t* ht = reinterpret_cast<uint16_t*>(smem);
+      typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+      if (mma_wave) {
 #pragma unroll
-  for (int e = 0; e < EP; ++e) {
+        for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+          for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const int row = wm * WTM + fm * 32 + fr;
+              const int col = (wn * FN + fn) * 32 + 8 * q + 4 * fh;
+              const f32x16& a = acc[fm][fn];
+              const u32x2 w = {
+                  __builtin_bit_cast(uint32_t, h2{(_Float16)a[4 * q], (_Float16)a[4 * q + 1]}),
+                  __builtin_bit_cast(uint32_t, h2{(_Float16)a[4 * q + 2], (_Float16)a[4 * q + 3]})};
+              *reinterpret_cast<u32x2*>(ht + row * LDH + col) = w;
+            }
+      }
+      __syncthreads();
+#ifdef QA_PHASE_STAMPS
+      st[3] = __builtin_amdgcn_s_memrealtime();
+#endif
+#pragma unroll
+      for (int it = 0; it < (BM * GPR + NTH - 1) / NTH; ++it) {
+        const int idx = it * NTH + tid;
+        if (BM * GPR % NTH != 0 && idx >= BM * GPR) break;
+        const int r = idx / GPR, c4 = (idx % GPR) * 4;
+        const int m = m0 + r, n = n0 + c4;
+        if (m >= p.M || n >= nfull) continue;
+        const u32x2 g = *reinterpret_cast<const u32x2*>(ht + r * LDH + c4);
+        const u32x2 u = *reinterpret_cast<const u32x2*>(ht + r * LDH + BN / 2 + c4);
+        const u32x2 w = {silu_mul_h2(g.x, u.x), silu_mul_h2(g.y, u.y)};
+        asm volatile("global_store_dwordx2 %0, %1, off sc1" ::"v"(C + (int64_t)m * p.ldc + n),
+                     "v"(w)
+                     : "memory");
+      }
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < (parked16 ? 0 : EP); ++e) {
     if (e > 0) __syncthreads();  // the previous pass's rows have been read
 #pragma unroll
     for (int g = 0; g < KG; ++g) {

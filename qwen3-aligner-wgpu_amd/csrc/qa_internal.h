@@ -140,10 +140,11 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
 // transcendental (v_rcp_f32): the compiler inserts it ahead of its own
 // instructions but not ahead of an asm statement, which without it read the
 // register's previous value (1 + 2^t).
-__device__ __forceinline__ uint32_t silu_mul_f16x2(float g0, float g1, float u0, float u1) {
+// silu_mul_h2 takes g and u already rounded and packed (gw, uw: two f16
+// each, element 0 in the low half); gw and uw must not come straight from a
+// transcendental or an MFMA (an asm statement gets no wait state ahead of it).
+__device__ __forceinline__ uint32_t silu_mul_h2(uint32_t gw, uint32_t uw) {
   typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-  const uint32_t gw = __builtin_bit_cast(uint32_t, h2{(_Float16)g0, (_Float16)g1});
-  const uint32_t uw = __builtin_bit_cast(uint32_t, h2{(_Float16)u0, (_Float16)u1});
   const float c = -1.44269504088896341f;
   float t0, t1, s0, s1, p0, p1;
   asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[1,0,0]" : "=v"(t0) : "v"(gw), "v"(c));
@@ -156,6 +157,11 @@ __device__ __forceinline__ uint32_t silu_mul_f16x2(float g0, float g1, float u0,
   asm("v_fma_mix_f32 %0, %1, %2, neg(0) op_sel_hi:[0,1,0]" : "=v"(p0) : "v"(s0), "v"(uw));
   asm("v_fma_mix_f32 %0, %1, %2, neg(0) op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "=v"(p1) : "v"(s1), "v"(uw));
   return __builtin_bit_cast(uint32_t, h2{(_Float16)p0, (_Float16)p1});
+}
+__device__ __forceinline__ uint32_t silu_mul_f16x2(float g0, float g1, float u0, float u1) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  return silu_mul_h2(__builtin_bit_cast(uint32_t, h2{(_Float16)g0, (_Float16)g1}),
+                     __builtin_bit_cast(uint32_t, h2{(_Float16)u0, (_Float16)u1}));
 }
 
 // Kernel parameters (passed by value).  Element units throughout.
