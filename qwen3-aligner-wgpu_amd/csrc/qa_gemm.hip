@@ -782,22 +782,34 @@ __global__ void __launch_bounds__(64 * (WGM * WGN * KG + PW)) gemm_dma_kernel(co
   constexpr int GPR = OUTC / 4;                          // 4-column groups per row
   const int nfull = EPI == EPI_SILU ? p.N / 2 : p.N;
   const int n0 = tn * OUTC;
+  // The column bias in LDS for the 16-bit park below (the MMA lanes' column
+  // order): the words thread t < BN / 4 preloaded for its store groups.
+  constexpr bool PK16 = KG == 1 && ((EPI == EPI_SILU && DT == QA_F16) || EPI == EPI_PLAIN ||
+                                    EPI == EPI_GELU);
+  __shared__ u32x2 sbias[PK16 && BPRE ? EGPR : 1];
+  if constexpr (PK16 && BPRE) {
+    if (tid < EGPR) sbias[tid] = tn * BN + tid * 4 < p.N ? bpre[0] : u32x2{0, 0};
+  }
   __syncthreads();  // all stages consumed (every DMA was waited for)
 #ifdef QA_PHASE_STAMPS
   st[2] = __builtin_amdgcn_s_memrealtime();
 #endif
-  // f16 SiLU.up, unsplit, one k group: the epilogue rounds g and u to f16
-  // before anything else, so the MMA waves park them rounded, as an f16
+  // 16-bit park (unsplit launches with one k group and no residual): the MMA
+  // waves finish each output in registers and park it rounded, as a 16-bit
   // [BM][BN + 4] tile: half the LDS bytes of the f32 tile, in one pass where
-  // the f32 tile of a 256-row tile needs two, and the store loop reads packed
-  // pairs straight into silu_mul_h2 (no conversions).  Same bits as the f32
-  // path below, which split launches (f32 partials) still take.
+  // the f32 tile of a 256-row tile needs two.  Plain and GELU outputs get
+  // their bias (from sbias) and GELU in the MMA lanes, in f32, then the one
+  // rounding; the store loop only copies rows out.  f16 SiLU.up parks g and u
+  // rounded (the epilogue's first step) and the store loop reads the packed
+  // pairs straight into silu_mul_h2.  Same bits as the f32 path below, which
+  // split launches (f32 partials), residual adds and channel-major bias take.
   bool parked16 = false;
-  if constexpr (EPI == EPI_SILU && DT == QA_F16 && KG == 1) {
-    if (p.splits == 1) {
+  if constexpr (PK16) {
+    if (p.splits == 1 &&
+        (EPI == EPI_SILU || (!p.accumulate && !p.bias_rows && (BPRE || !p.bias)))) {
       parked16 = true;
-      constexpr int LDH = BN + 4;  // halves per parked row
-      static_assert(BM * LDH * 2 <= SMEM, "f16 park fits the LDS");
+      constexpr int LDH = BN + 4;  // 16-bit values per parked row
+      static_assert(BM * LDH * 2 <= SMEM, "16-bit park fits the LDS");
       uint16_t* ht = reinterpret_cast<uint16_t*>(smem);
       typedef _Float16 h2 __attribute__((ext_vector_type(2)));
       if (mma_wave) {
@@ -809,10 +821,29 @@ __global__ void __launch_bounds__(64 * (WGM * WGN * KG + PW)) gemm_dma_kernel(co
             for (int q = 0; q < 4; ++q) {
               const int row = wm * WTM + fm * 32 + fr;
               const int col = (wn * FN + fn) * 32 + 8 * q + 4 * fh;
-              const f32x16& a = acc[fm][fn];
-              const u32x2 w = {
-                  __builtin_bit_cast(uint32_t, h2{(_Float16)a[4 * q], (_Float16)a[4 * q + 1]}),
-                  __builtin_bit_cast(uint32_t, h2{(_Float16)a[4 * q + 2], (_Float16)a[4 * q + 3]})};
+              float x[4];
+#pragma unroll
+              for (int e = 0; e < 4; ++e) x[e] = acc[fm][fn][4 * q + e];
+              if constexpr (EPI != EPI_SILU) {
+                if constexpr (BPRE) {
+                  float b[4];
+                  widen4<DT>(sbias[col >> 2], b);
+#pragma unroll
+                  for (int e = 0; e < 4; ++e) x[e] += b[e];
+                }
+                if constexpr (EPI == EPI_GELU) {
+#pragma unroll
+                  for (int e = 0; e < 4; ++e) x[e] = gelu_erf(x[e]);
+                }
+              }
+              u32x2 w;
+              if constexpr (DT == QA_F16) {
+                w.x = __builtin_bit_cast(uint32_t, h2{(_Float16)x[0], (_Float16)x[1]});
+                w.y = __builtin_bit_cast(uint32_t, h2{(_Float16)x[2], (_Float16)x[3]});
+              } else {
+                w.x = Fmt<DT>::narrow(x[0]) | (Fmt<DT>::narrow(x[1]) << 16);
+                w.y = Fmt<DT>::narrow(x[2]) | (Fmt<DT>::narrow(x[3]) << 16);
+              }
               *reinterpret_cast<u32x2*>(ht + row * LDH + col) = w;
             }
       }
@@ -827,9 +858,11 @@ __global__ void __launch_bounds__(64 * (WGM * WGN * KG + PW)) gemm_dma_kernel(co
         const int r = idx / GPR, c4 = (idx % GPR) * 4;
         const int m = m0 + r, n = n0 + c4;
         if (m >= p.M || n >= nfull) continue;
-        const u32x2 g = *reinterpret_cast<const u32x2*>(ht + r * LDH + c4);
-        const u32x2 u = *reinterpret_cast<const u32x2*>(ht + r * LDH + BN / 2 + c4);
-        const u32x2 w = {silu_mul_h2(g.x, u.x), silu_mul_h2(g.y, u.y)};
+        u32x2 w = *reinterpret_cast<const u32x2*>(ht + r * LDH + c4);
+        if constexpr (EPI == EPI_SILU) {
+          const u32x2 u = *reinterpret_cast<const u32x2*>(ht + r * LDH + BN / 2 + c4);
+          w = u32x2{silu_mul_h2(w.x, u.x), silu_mul_h2(w.y, u.y)};
+        }
         asm volatile("global_store_dwordx2 %0, %1, off sc1" ::"v"(C + (int64_t)m * p.ldc + n),
                      "v"(w)
                      : "memory");
