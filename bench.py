@@ -753,6 +753,29 @@ def bench_e2e(pkg, ctx, warmup, steps):
     return out
 
 
+def e2e_eager(pkg, ctx, warmup, steps):
+    """The config-5 forward of bench_e2e, launched eagerly (no hipGraph):
+    `warmup` then `steps` forwards, timed by HIP events and the host clock.
+    For kernel traces: each kernel then appears once per forward, in launch
+    order, with no graph machinery in the process."""
+    from qwen3_aligner_wgpu_amd import synthetic as syn
+    c = E2E
+    w = syn.aligner_weights(c["dtype"], c["enc_layers"], c["dec_layers"], c["seed"])
+    x = syn.synthetic_audio(c["seconds"], c["seed"])
+    words = [syn.word_token_ids(t) for t in syn.synthetic_words(c["words"], c["seed"])]
+    al, enc, dec = syn.build_aligner(pkg, ctx, c["dtype"], w, c["seconds"] + 0.01, max(PREFILL_ROWS))
+    del w
+    try:
+        al.prepare(x, words)
+        ev_ms, wall_ms = al.time(warmup, steps, use_graph=False)
+    finally:
+        al.close()
+        enc.close()
+        dec.close()
+    return {"eager_ms": round(max(ev_ms, wall_ms), 3), "event_ms": round(ev_ms, 3),
+            "wall_ms": round(wall_ms, 3), "warmup": warmup, "steps": steps}
+
+
 def bench_encoder(pkg, host, ctx, m, warmup, steps):
     dt = pkg.BF16
     d, f, ck = ENC["d_model"], ENC["ffn"], ENC["conv_k"]
@@ -827,6 +850,9 @@ def main():
     ap.add_argument("--no-detail", action="store_true", help="skip configs 1, 2, 4")
     ap.add_argument("--e2e-only", action="store_true",
                     help="only the config-5 aligner forward (for profiling); prints its detail")
+    ap.add_argument("--e2e-eager", action="store_true",
+                    help="only the config-5 forward, launched eagerly without a graph, --warmup "
+                         "then --steps times (for kernel traces); prints one JSON line")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 512 MiB copy 3 times (calibrates FETCH_SIZE/WRITE_SIZE)")
     ap.add_argument("--site", default=None,
@@ -866,6 +892,11 @@ def main():
 
     pkg = entry.load_package()
     from qwen3_aligner_wgpu_amd import host
+
+    if args.e2e_eager:
+        with pkg.Context(0) as ctx:
+            print(json.dumps(e2e_eager(pkg, ctx, args.warmup, args.steps)), flush=True)
+        return
 
     if args.copy_calibration:
         with pkg.Context(0) as ctx:
