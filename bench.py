@@ -753,11 +753,12 @@ def bench_e2e(pkg, ctx, warmup, steps):
     return out
 
 
-def e2e_eager(pkg, ctx, warmup, steps):
+def e2e_eager(pkg, ctx, warmup, steps, p16=False):
     """The config-5 forward of bench_e2e, launched eagerly (no hipGraph):
     `warmup` then `steps` forwards, timed by HIP events and the host clock.
     For kernel traces: each kernel then appears once per forward, in launch
-    order, with no graph machinery in the process."""
+    order, with no graph machinery in the process.  p16: the attention's
+    probabilities rounded once to 16 bits (QA_ATTN_P16)."""
     from qwen3_aligner_wgpu_amd import synthetic as syn
     c = E2E
     w = syn.aligner_weights(c["dtype"], c["enc_layers"], c["dec_layers"], c["seed"])
@@ -767,13 +768,15 @@ def e2e_eager(pkg, ctx, warmup, steps):
     del w
     try:
         al.prepare(x, words)
+        if p16:
+            dec.set_attention_flags(pkg.QA_ATTN_P16)
         ev_ms, wall_ms = al.time(warmup, steps, use_graph=False)
     finally:
         al.close()
         enc.close()
         dec.close()
     return {"eager_ms": round(max(ev_ms, wall_ms), 3), "event_ms": round(ev_ms, 3),
-            "wall_ms": round(wall_ms, 3), "warmup": warmup, "steps": steps}
+            "wall_ms": round(wall_ms, 3), "warmup": warmup, "steps": steps, "attn_p16": p16}
 
 
 def bench_encoder(pkg, host, ctx, m, warmup, steps):
@@ -853,6 +856,8 @@ def main():
     ap.add_argument("--e2e-eager", action="store_true",
                     help="only the config-5 forward, launched eagerly without a graph, --warmup "
                          "then --steps times (for kernel traces); prints one JSON line")
+    ap.add_argument("--attn-p16", action="store_true",
+                    help="with --e2e-eager: the attention's probabilities rounded once to 16 bits")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 512 MiB copy 3 times (calibrates FETCH_SIZE/WRITE_SIZE)")
     ap.add_argument("--site", default=None,
@@ -895,7 +900,7 @@ def main():
 
     if args.e2e_eager:
         with pkg.Context(0) as ctx:
-            print(json.dumps(e2e_eager(pkg, ctx, args.warmup, args.steps)), flush=True)
+            print(json.dumps(e2e_eager(pkg, ctx, args.warmup, args.steps, args.attn_p16)), flush=True)
         return
 
     if args.copy_calibration:
