@@ -753,6 +753,52 @@ def bench_e2e(pkg, ctx, warmup, steps):
     return out
 
 
+def attention_stamps(pkg, host, ctx):
+    """The decoder attention at s = 4352 (16 q heads, 8 kv heads, hd 128, f16,
+    synthetic q / K / V) on the measurement build, in both probability modes:
+    every wave's s_memtime cycles by phase (qa_attn_stamps_read), as medians
+    over the waves -- per MFMA phase and per VALU phase, and each phase
+    kind's share of a wave's cycles."""
+    L = pkg.lib()
+    L.qa_attn_stamps_read.argtypes = [ctypes.c_void_p] * 4
+    nb, nw, nwd = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    pkg.check(L.qa_attn_stamps_read(None, ctypes.byref(nb), ctypes.byref(nw), ctypes.byref(nwd)))
+    rows, nqh, nkvh, hd = 4352, 16, 8, 128
+    q = ctx.to_device(host.synth_normal(0, 1, (nqh, rows, hd), 0, 0.3))
+    kc = ctx.to_device(host.synth_normal(0, 2, (nkvh, rows, hd)))
+    vc = ctx.to_device(host.synth_normal(0, 3, (nkvh, hd, rows)))
+    out = ctx.alloc(rows * nqh * hd * 2)
+    res = {}
+    for name, flags in (("two-term P (default)", 0), ("single-rounded P", pkg.QA_ATTN_P16)):
+        desc = pkg.AttentionDesc(dtype=pkg.F16, flags=flags, rows=rows, nqh=nqh, nkvh=nkvh, hd=hd,
+                                 q=int(q), k_cache=int(kc), v_cache=int(vc), cap=rows, q0=0,
+                                 out=int(out), ldo=nqh * hd)
+        for _ in range(3):
+            ctx.attention_prefill(desc)
+        ctx.sync()
+        pkg.check(L.qa_attn_stamps_clear())
+        ctx.attention_prefill(desc)
+        ctx.sync()
+        rec = np.zeros((nb.value, nw.value, nwd.value), np.uint64)
+        pkg.check(L.qa_attn_stamps_read(rec.ctypes.data, None, None, None))
+        r = rec.reshape(-1, nwd.value).astype(np.float64)
+        r = r[r[:, 6] > 0]  # waves that ran at least one MFMA phase
+        tot = r[:, :6].sum(axis=1)
+        med = lambda x: round(float(np.median(x)), 3)  # noqa: E731
+        res[name] = {
+            "waves": int(len(r)),
+            "cycles_per_mfma_phase": med(r[:, 1] / r[:, 6]),
+            "cycles_per_valu_phase": med(r[r[:, 7] > 0, 2] / r[r[:, 7] > 0, 7]),
+            "share": {k: med(r[:, i] / tot) for i, k in enumerate(
+                ("prologue", "mfma_phases", "valu_phases", "no_work_phases", "waits", "merge_and_output"))},
+            "mfma_phases_per_wave": med(r[:, 6]),
+            "wave_cycles": med(tot),
+        }
+    for b in (q, kc, vc, out):
+        b.free()
+    return res
+
+
 def e2e_eager(pkg, ctx, warmup, steps, p16=False):
     """The config-5 forward of bench_e2e, launched eagerly (no hipGraph):
     `warmup` then `steps` forwards, timed by HIP events and the host clock.
@@ -856,6 +902,10 @@ def main():
     ap.add_argument("--e2e-eager", action="store_true",
                     help="only the config-5 forward, launched eagerly without a graph, --warmup "
                          "then --steps times (for kernel traces); prints one JSON line")
+    ap.add_argument("--attn-stamps", action="store_true",
+                    help="the decoder attention at s = 4352 on the measurement build (make -C "
+                         "qwen3-aligner-wgpu_amd/csrc stamps): each wave's cycles by phase, both "
+                         "probability modes (one JSON line)")
     ap.add_argument("--attn-p16", action="store_true",
                     help="with --e2e-eager: the attention's probabilities rounded once to 16 bits")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -887,7 +937,7 @@ def main():
               "token rows with no exchange; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
-    if args.phase_stamps or args.phase_stamps_prefill:
+    if args.phase_stamps or args.phase_stamps_prefill or args.attn_stamps:
         os.environ["QA_BUILD"] = "stamps"  # before the package loads its libraries
     if args.vs_hipblaslt:
         # torch's own HIP runtime and BLAS libraries first: loaded after this
@@ -897,6 +947,11 @@ def main():
 
     pkg = entry.load_package()
     from qwen3_aligner_wgpu_amd import host
+
+    if args.attn_stamps:
+        with pkg.Context(0) as ctx:
+            print(json.dumps(attention_stamps(pkg, host, ctx)), flush=True)
+        return
 
     if args.e2e_eager:
         with pkg.Context(0) as ctx:

@@ -21,7 +21,8 @@ import numpy as np
 _HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(_HERE, "csrc")
 # QA_BUILD=stamps loads the measurement build of `make -C csrc stamps` (the
-# same libraries with per-block phase stamps in the GEMM kernels).
+# same libraries with per-block phase stamps in the GEMM kernels and per-wave
+# phase cycles in the attention kernel).
 _BUILD_DIR = os.path.join(CSRC, os.environ["QA_BUILD"]) if os.environ.get("QA_BUILD") else CSRC
 LIB_PATH = os.path.join(_BUILD_DIR, "libqa.so")
 HOST_LIB_PATH = os.path.join(_BUILD_DIR, "libqa_host.so")

@@ -40,6 +40,17 @@
 #include "qa_internal.h"
 
 namespace qa {
+
+#ifdef QA_PHASE_STAMPS
+// Measurement build only (make stamps): every wave of an attention_kernel
+// launch adds up s_memtime (shader clock) cycles by phase -- the prologue up
+// to the phase loop, the MFMA phases (P.V + S issued), the VALU phases
+// (softmax, DMA issue), the phases with no work of its own, the waits after
+// each phase (DMA, LDS, block barrier), and the merge and output -- and counts
+// its MFMA and VALU phases.  Words per wave: those six sums, the two counts.
+constexpr int kAttnStampBlocks = 2048, kAttnStampWaves = 8, kAttnStampWords = 8;
+__device__ unsigned long long attn_stamp_log[kAttnStampBlocks * kAttnStampWaves * kAttnStampWords];
+#endif
 namespace {
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -174,6 +185,13 @@ __global__ void __launch_bounds__(NS * REP * 2 * 64) attention_kernel(const Attn
   const int split = wave / GW, wg = wave % GW;
   const int hh = wg / 2, rg = wg & 1;
   const int fr = lane & 31, fh = lane >> 5;
+#ifdef QA_PHASE_STAMPS
+  // s_memtime cycles by phase: prologue, MFMA, VALU, no work, waits, merge
+  unsigned long long cyc[6] = {0, 0, 0, 0, 0, 0}, nmma = 0, nvalu = 0;
+  __builtin_amdgcn_sched_barrier(0);
+  unsigned long long c_mark = __builtin_amdgcn_s_memtime();
+  __builtin_amdgcn_sched_barrier(0);
+#endif
 
   // Block b -> kv head b % nkvh, row tile T - 1 - b / nkvh: the longest key
   // ranges of every head are dispatched first, and with blocks dealt
@@ -427,8 +445,21 @@ __global__ void __launch_bounds__(NS * REP * 2 * 64) attention_kernel(const Attn
   if (nst > 0) issue_v(0);
   if (split == 0) wait_refill(refill_count(-1));
   exec_barrier();
+#ifdef QA_PHASE_STAMPS
+  auto stamp = [&](int bucket) {  // charge the cycles since the last mark to a bucket
+    __builtin_amdgcn_sched_barrier(0);
+    const unsigned long long now = __builtin_amdgcn_s_memtime();
+    __builtin_amdgcn_sched_barrier(0);
+    cyc[bucket] += now - c_mark;
+    c_mark = now;
+  };
+  stamp(0);
+#endif
   for (int ph = 0; ph < phases; ++ph) {
     const int my = ph - split;
+#ifdef QA_PHASE_STAMPS
+    int bucket = 3;
+#endif
     if (my >= 0 && my <= 2 * nst) {
       const int it = my >> 1;
       if ((my & 1) == 0) {
@@ -438,16 +469,30 @@ __global__ void __launch_bounds__(NS * REP * 2 * 64) attention_kernel(const Attn
           mma(F_{}, T_{}, it);
         else if (it == nst && it >= 1)
           mma(T_{}, F_{}, it);
+#ifdef QA_PHASE_STAMPS
+        bucket = 1;
+        ++nmma;
+#endif
       } else {
         if (it + 2 < nst) issue_k(it + 2);
         if (it + 1 < nst) issue_v(it + 1);
         softmax(it);
+#ifdef QA_PHASE_STAMPS
+        bucket = 2;
+        ++nvalu;
+#endif
       }
     }
+#ifdef QA_PHASE_STAMPS
+    stamp(bucket);
+#endif
     const int nx = ph + 1 - split;  // this wave's next phase
     if (nx >= 0 && (nx & 1) == 0 && (nx >> 1) <= nst) wait_refill(refill_count((nx >> 1) - 1));
     wait_lds();
     exec_barrier();
+#ifdef QA_PHASE_STAMPS
+    stamp(4);
+#endif
   }
 
   // ---- merge the two key splits (fixed order) and write the output ----
@@ -484,6 +529,16 @@ __global__ void __launch_bounds__(NS * REP * 2 * 64) attention_kernel(const Attn
         *reinterpret_cast<u32x2*>(out + dt * 32 + 8 * g + 4 * fh) = pk;
       }
   }
+#ifdef QA_PHASE_STAMPS
+  stamp(5);
+  if (lane == 0 && blockIdx.x < (unsigned)kAttnStampBlocks && wave < kAttnStampWaves) {
+    unsigned long long* d =
+        attn_stamp_log + ((size_t)blockIdx.x * kAttnStampWaves + wave) * kAttnStampWords;
+    for (int i = 0; i < 6; ++i) d[i] = cyc[i];
+    d[6] = nmma;
+    d[7] = nvalu;
+  }
+#endif
 }
 
 }  // namespace
@@ -511,3 +566,25 @@ hipError_t launch_attention(int dtype, const AttnParams& p, bool p16, hipStream_
 }
 
 }  // namespace qa
+
+#ifdef QA_PHASE_STAMPS
+// The measurement build's attention records: kAttnStampBlocks x
+// kAttnStampWaves x kAttnStampWords words (see attn_stamp_log), copied to
+// `out`; *blocks, *waves and *words get the sizes.
+extern "C" int qa_attn_stamps_read(unsigned long long* out, int* blocks, int* waves, int* words) {
+  if (blocks) *blocks = qa::kAttnStampBlocks;
+  if (waves) *waves = qa::kAttnStampWaves;
+  if (words) *words = qa::kAttnStampWords;
+  if (!out) return QA_OK;
+  const hipError_t e =
+      hipMemcpyFromSymbol(out, HIP_SYMBOL(qa::attn_stamp_log), sizeof(qa::attn_stamp_log));
+  return e == hipSuccess ? QA_OK : QA_EDEVICE;
+}
+// Zeroes every record (synchronous; call outside stream capture).
+extern "C" int qa_attn_stamps_clear(void) {
+  static unsigned long long zeros[sizeof(qa::attn_stamp_log) / 8];
+  const hipError_t e =
+      hipMemcpyToSymbol(HIP_SYMBOL(qa::attn_stamp_log), zeros, sizeof(qa::attn_stamp_log));
+  return e == hipSuccess ? QA_OK : QA_EDEVICE;
+}
+#endif
