@@ -782,16 +782,17 @@ def attention_stamps(pkg, host, ctx):
         rec = np.zeros((nb.value, nw.value, nwd.value), np.uint64)
         pkg.check(L.qa_attn_stamps_read(rec.ctypes.data, None, None, None))
         r = rec.reshape(-1, nwd.value).astype(np.float64)
-        r = r[r[:, 6] > 0]  # waves that ran at least one MFMA phase
-        tot = r[:, :6].sum(axis=1)
+        r = r[r[:, 7] > 0]  # waves that ran at least one MFMA phase
+        tot = r[:, :7].sum(axis=1)
         med = lambda x: round(float(np.median(x)), 3)  # noqa: E731
         res[name] = {
             "waves": int(len(r)),
-            "cycles_per_mfma_phase": med(r[:, 1] / r[:, 6]),
-            "cycles_per_valu_phase": med(r[r[:, 7] > 0, 2] / r[r[:, 7] > 0, 7]),
+            "cycles_per_mfma_phase": med(r[:, 1] / r[:, 7]),
+            "cycles_per_valu_phase": med(r[r[:, 8] > 0, 2] / r[r[:, 8] > 0, 8]),
             "share": {k: med(r[:, i] / tot) for i, k in enumerate(
-                ("prologue", "mfma_phases", "valu_phases", "no_work_phases", "waits", "merge_and_output"))},
-            "mfma_phases_per_wave": med(r[:, 6]),
+                ("prologue", "mfma_phases", "valu_phases", "no_work_phases", "barrier",
+                 "merge_and_output", "dma_lds_waits"))},
+            "mfma_phases_per_wave": med(r[:, 7]),
             "wave_cycles": med(tot),
         }
     for b in (q, kc, vc, out):

@@ -45,10 +45,11 @@ namespace qa {
 // Measurement build only (make stamps): every wave of an attention_kernel
 // launch adds up s_memtime (shader clock) cycles by phase -- the prologue up
 // to the phase loop, the MFMA phases (P.V + S issued), the VALU phases
-// (softmax, DMA issue), the phases with no work of its own, the waits after
-// each phase (DMA, LDS, block barrier), and the merge and output -- and counts
-// its MFMA and VALU phases.  Words per wave: those six sums, the two counts.
-constexpr int kAttnStampBlocks = 2048, kAttnStampWaves = 8, kAttnStampWords = 8;
+// (softmax, DMA issue), the phases with no work of its own, the block
+// barrier after each phase, the merge and output, and the DMA and LDS waits
+// before each barrier -- and counts its MFMA and VALU phases.  Words per
+// wave: those seven sums, the two counts.
+constexpr int kAttnStampBlocks = 2048, kAttnStampWaves = 8, kAttnStampWords = 9;
 __device__ unsigned long long attn_stamp_log[kAttnStampBlocks * kAttnStampWaves * kAttnStampWords];
 #endif
 namespace {
@@ -186,8 +187,9 @@ __global__ void __launch_bounds__(NS * REP * 2 * 64) attention_kernel(const Attn
   const int hh = wg / 2, rg = wg & 1;
   const int fr = lane & 31, fh = lane >> 5;
 #ifdef QA_PHASE_STAMPS
-  // s_memtime cycles by phase: prologue, MFMA, VALU, no work, waits, merge
-  unsigned long long cyc[6] = {0, 0, 0, 0, 0, 0}, nmma = 0, nvalu = 0;
+  // s_memtime cycles by phase: prologue, MFMA, VALU, no work, barrier,
+  // merge, DMA + LDS waits
+  unsigned long long cyc[7] = {0, 0, 0, 0, 0, 0, 0}, nmma = 0, nvalu = 0;
   __builtin_amdgcn_sched_barrier(0);
   unsigned long long c_mark = __builtin_amdgcn_s_memtime();
   __builtin_amdgcn_sched_barrier(0);
@@ -489,6 +491,9 @@ __global__ void __launch_bounds__(NS * REP * 2 * 64) attention_kernel(const Attn
     const int nx = ph + 1 - split;  // this wave's next phase
     if (nx >= 0 && (nx & 1) == 0 && (nx >> 1) <= nst) wait_refill(refill_count((nx >> 1) - 1));
     wait_lds();
+#ifdef QA_PHASE_STAMPS
+    stamp(6);
+#endif
     exec_barrier();
 #ifdef QA_PHASE_STAMPS
     stamp(4);
@@ -534,9 +539,9 @@ __global__ void __launch_bounds__(NS * REP * 2 * 64) attention_kernel(const Attn
   if (lane == 0 && blockIdx.x < (unsigned)kAttnStampBlocks && wave < kAttnStampWaves) {
     unsigned long long* d =
         attn_stamp_log + ((size_t)blockIdx.x * kAttnStampWaves + wave) * kAttnStampWords;
-    for (int i = 0; i < 6; ++i) d[i] = cyc[i];
-    d[6] = nmma;
-    d[7] = nvalu;
+    for (int i = 0; i < 7; ++i) d[i] = cyc[i];
+    d[7] = nmma;
+    d[8] = nvalu;
   }
 #endif
 }
